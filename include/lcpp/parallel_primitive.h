@@ -1,0 +1,242 @@
+/*
+ * lcpp/parallel_primitive.h — the reference's C++ host API over the C ABI.
+ *
+ * Same class, method and argument names as src/lcpp/device/device_*.h of
+ * Ligo04/lc_parallel_primitive (umbrella header src/lcpp/parallel_primitive.h),
+ * so code written against the reference switches by changing its types:
+ *
+ *   reference (LuisaCompute)                 here (HIP)
+ *   ---------------------------------------  ------------------------------------
+ *   Device / Stream                          Device{ordinal} / Stream{hipStream_t}
+ *   CommandList& cmdlist                     CommandList{hipStream_t}: work is
+ *                                            enqueued on the stream at the call
+ *   BufferView<T>                            BufferView<T>{T* device pointer, count}
+ *   BufferView<uint> temp_storage            caller-owned, Get*TempStorageBytes
+ *
+ * Errors: the reference asserts in debug builds (lcpp_check, runtime/core.h
+ * :56-67) and ignores failures in release.  Here every call returns through
+ * check(): debug builds print the status and abort, release builds keep the
+ * last status, readable with last_status().
+ *
+ * Template parameters <BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD> are accepted
+ * for source compatibility; the geometry is fixed per dtype inside the
+ * library (64-lane waves, tuned for gfx950).
+ */
+#ifndef LCPP_PARALLEL_PRIMITIVE_H
+#define LCPP_PARALLEL_PRIMITIVE_H
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <type_traits>
+
+#include "../lcpp_amd.h"
+
+namespace luisa::parallel_primitive {
+
+using uint = unsigned int;
+
+template <class T>
+struct BufferView {
+    T *ptr = nullptr;
+    size_t count = 0;
+    BufferView() = default;
+    BufferView(T *p, size_t n) : ptr(p), count(n) {}
+    [[nodiscard]] size_t size() const noexcept { return count; }
+    [[nodiscard]] size_t size_bytes() const noexcept { return count * sizeof(T); }
+    [[nodiscard]] T *data() const noexcept { return ptr; }
+    [[nodiscard]] BufferView subview(size_t offset, size_t n) const noexcept { return {ptr + offset, n}; }
+};
+
+struct Device {
+    int ordinal = 0;
+};
+struct Stream {
+    void *handle = nullptr; /* hipStream_t */
+};
+struct CommandList {
+    void *stream = nullptr; /* hipStream_t; work is enqueued here at the call */
+};
+
+template <class T>
+constexpr lcpp_dtype dtype_of()
+{
+    using U = std::remove_cv_t<T>;
+    if constexpr (std::is_same_v<U, float>) return LCPP_FLOAT32;
+    else if constexpr (std::is_same_v<U, double>) return LCPP_FLOAT64;
+    else if constexpr (std::is_integral_v<U> && sizeof(U) == 4 && std::is_signed_v<U>) return LCPP_INT32;
+    else if constexpr (std::is_integral_v<U> && sizeof(U) == 4) return LCPP_UINT32;
+    else if constexpr (std::is_integral_v<U> && sizeof(U) == 8 && std::is_signed_v<U>) return LCPP_INT64;
+    else if constexpr (std::is_integral_v<U> && sizeof(U) == 8) return LCPP_UINT64;
+    else static_assert(sizeof(U) == 0, "NumericT: 4- or 8-byte integer or floating type");
+}
+
+/* bytes -> count of uint words, as the reference's bytes_to_uint_count (common/utils.h:166-169) */
+inline size_t bytes_to_uint_count(size_t bytes) { return (bytes + sizeof(uint) - 1) / sizeof(uint); }
+
+namespace details {
+constexpr size_t BLOCK_SIZE = 256;
+constexpr size_t WARP_SIZE = 64;
+constexpr size_t ITEMS_PER_THREAD = 16;
+}  // namespace details
+
+class LuisaModule {
+  public:
+    void create(Device &device, Stream *debug_stream = nullptr)
+    {
+        m_device = device;
+        m_debug_stream = debug_stream;
+        m_created = true;
+    }
+    [[nodiscard]] int last_status() const noexcept { return m_last_status; }
+
+  protected:
+    void check(int status, const char *what)
+    {
+        m_last_status = status;
+#ifndef NDEBUG
+        if (status != LCPP_OK) {
+            std::fprintf(stderr, "lcpp: %s failed: %s\n", what, lcpp_status_string(status));
+            std::abort();
+        }
+#else
+        (void)what;
+#endif
+    }
+    Device m_device{};
+    Stream *m_debug_stream = nullptr;
+    bool m_created = false;
+    int m_last_status = LCPP_OK;
+};
+
+/* device/device_reduce.h:37-185 */
+template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
+          size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
+class DeviceReduce : public LuisaModule {
+  public:
+    template <class T>
+    static size_t GetTempStorageBytes(size_t num_item)
+    {
+        size_t b = 0;
+        lcpp_reduce_temp_bytes(dtype_of<T>(), num_item, &b);
+        return b;
+    }
+    template <class T>
+    void Sum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out, size_t num_item)
+    {
+        check(lcpp_reduce_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
+                              num_item, cmdlist.stream),
+              "DeviceReduce::Sum");
+    }
+    template <class T>
+    void Min(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out, size_t num_item)
+    {
+        check(lcpp_reduce_min(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
+                              num_item, cmdlist.stream),
+              "DeviceReduce::Min");
+    }
+    template <class T>
+    void Max(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out, size_t num_item)
+    {
+        check(lcpp_reduce_max(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
+                              num_item, cmdlist.stream),
+              "DeviceReduce::Max");
+    }
+};
+
+/* device/device_scan.h:33-204 */
+template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
+          size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
+class DeviceScan : public LuisaModule {
+  public:
+    template <class T>
+    static size_t GetTempStorageBytes(size_t num_items)
+    {
+        size_t b = 0;
+        lcpp_scan_temp_bytes(dtype_of<T>(), num_items, &b);
+        return b;
+    }
+    template <class T>
+    void ExclusiveSum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                      size_t num_items)
+    {
+        check(lcpp_scan_exclusive_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
+                                      d_out.data(), num_items, cmdlist.stream),
+              "DeviceScan::ExclusiveSum");
+    }
+    template <class T>
+    void InclusiveSum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                      size_t num_items)
+    {
+        check(lcpp_scan_inclusive_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
+                                      d_out.data(), num_items, cmdlist.stream),
+              "DeviceScan::InclusiveSum");
+    }
+};
+
+/* device/device_radix_sort.h:37-153 */
+template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
+          size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
+class DeviceRadixSort : public LuisaModule {
+  public:
+    template <class KeyType, class ValueType>
+    static size_t GetSortPairsTempStorageBytes(uint num_items)
+    {
+        size_t b = 0;
+        lcpp_radix_sort_pairs_temp_bytes(dtype_of<KeyType>(), dtype_of<ValueType>(), num_items, &b);
+        return b;
+    }
+    template <class KeyType>
+    static size_t GetSortKeysTempStorageBytes(uint num_items)
+    {
+        size_t b = 0;
+        lcpp_radix_sort_keys_temp_bytes(dtype_of<KeyType>(), num_items, &b);
+        return b;
+    }
+    template <class KeyType, class ValueType>
+    void SortPairs(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                   BufferView<KeyType> d_keys_out, BufferView<ValueType> d_values_in,
+                   BufferView<ValueType> d_values_out, uint num_items)
+    {
+        check(lcpp_radix_sort_pairs(dtype_of<KeyType>(), dtype_of<ValueType>(), temp_storage.data(),
+                                    temp_storage.size_bytes(), d_keys_in.data(), d_keys_out.data(),
+                                    d_values_in.data(), d_values_out.data(), num_items, cmdlist.stream),
+              "DeviceRadixSort::SortPairs");
+    }
+    template <class KeyType>
+    void SortKeys(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                  BufferView<KeyType> d_keys_out, uint num_items)
+    {
+        check(lcpp_radix_sort_keys(dtype_of<KeyType>(), temp_storage.data(), temp_storage.size_bytes(),
+                                   d_keys_in.data(), d_keys_out.data(), num_items, cmdlist.stream),
+              "DeviceRadixSort::SortKeys");
+    }
+};
+
+/* device/device_segment_reduce.h:26-135 */
+template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
+          size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
+class DeviceSegmentReduce : public LuisaModule {
+  public:
+    template <class T>
+    static size_t GetTempStorageBytes(size_t /*num_item*/)
+    {
+        size_t b = 0;
+        lcpp_segment_reduce_temp_bytes(dtype_of<T>(), 0, &b);
+        return b;
+    }
+    template <class T>
+    void Sum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             uint num_segments, BufferView<uint> d_begin_offsets, BufferView<uint> d_end_offsets)
+    {
+        check(lcpp_segment_reduce_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
+                                      d_out.data(), num_segments, d_begin_offsets.data(), d_end_offsets.data(),
+                                      cmdlist.stream),
+              "DeviceSegmentReduce::Sum");
+    }
+};
+
+}  // namespace luisa::parallel_primitive
+
+#endif /* LCPP_PARALLEL_PRIMITIVE_H */

@@ -1,0 +1,137 @@
+/*
+ * lcpp_amd.h — C ABI of the MI355X-native (gfx950) device-level primitives.
+ *
+ * Every entry point here replaces a method of the reference's C++ class
+ * templates (paths relative to src/lcpp/ of Ligo04/lc_parallel_primitive).
+ * The reference has no C ABI of its own; the C++ wrapper in
+ * include/lcpp/parallel_primitive.h restores its class/method names on top
+ * of these functions.
+ *
+ * Conventions
+ *   - Every function returns an lcpp_status (0 = success, negative = error);
+ *     nothing is thrown across the ABI.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     All work is enqueued asynchronously on it; results are valid once the
+ *     stream is synchronized.  No call synchronizes the stream.
+ *   - The caller owns all memory, including temp storage sized by the
+ *     matching *_temp_bytes query.  The library never allocates device
+ *     memory on these paths.  Temp storage must be 256-byte aligned.
+ *   - Inputs are read only.  The sort preserves keys_in / values_in
+ *     (as the reference's DoubleBuffer ping-pong does).
+ *   - Calls that share one temp buffer must not overlap in time (the
+ *     look-back state lives in temp storage).  Calls with distinct temp
+ *     buffers are thread-safe.
+ *   - *_temp_bytes queries are pure host arithmetic and need no GPU.
+ */
+#ifndef LCPP_AMD_H
+#define LCPP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LCPP_AMD_VERSION 100 /* 1.0.0 */
+
+typedef enum lcpp_dtype {
+    LCPP_INT32 = 0,
+    LCPP_UINT32 = 1,
+    LCPP_FLOAT32 = 2,
+    LCPP_INT64 = 3,
+    LCPP_UINT64 = 4,
+    LCPP_FLOAT64 = 5
+} lcpp_dtype;
+
+typedef enum lcpp_status {
+    LCPP_OK = 0,
+    LCPP_ERR_INVALID_ARG = -1,      /* null pointer, misaligned temp, size out of range */
+    LCPP_ERR_TEMP_TOO_SMALL = -2,   /* temp_bytes < the *_temp_bytes query result */
+    LCPP_ERR_UNSUPPORTED_DTYPE = -3,
+    LCPP_ERR_HIP = -4               /* a HIP runtime call or kernel launch failed */
+} lcpp_status;
+
+/* Library version (LCPP_AMD_VERSION of the build). */
+int lcpp_version(void);
+/* Static, human-readable name of a status code. */
+const char *lcpp_status_string(int status);
+
+/* ---------------------------------------------------------------------
+ * DeviceReduce — device/device_reduce.h
+ * ------------------------------------------------------------------- */
+/* replaces DeviceReduce::GetTempStorageBytes<T>(num_item), device_reduce.h:85-91 */
+int lcpp_reduce_temp_bytes(lcpp_dtype t, uint64_t n, size_t *bytes);
+/* replaces DeviceReduce::Sum(cmdlist, temp, d_in, d_out, num_item), device_reduce.h:169-173
+ * out[0] = 0 + sum(in[0..n)); integers wrap (two's complement). */
+int lcpp_reduce_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                    uint64_t n, void *stream);
+/* replaces DeviceReduce::Min, device_reduce.h:175-179 (init = numeric max) */
+int lcpp_reduce_min(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                    uint64_t n, void *stream);
+/* replaces DeviceReduce::Max, device_reduce.h:181-185 (init = numeric lowest; the reference
+ * uses numeric_limits<T>::min(), which differs for floating point only) */
+int lcpp_reduce_max(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                    uint64_t n, void *stream);
+
+/* ---------------------------------------------------------------------
+ * DeviceScan — device/device_scan.h
+ * ------------------------------------------------------------------- */
+/* replaces DeviceScan::GetTempStorageBytes<T>(num_items), device_scan.h:76-89 */
+int lcpp_scan_temp_bytes(lcpp_dtype t, uint64_t n, size_t *bytes);
+/* replaces DeviceScan::ExclusiveSum, device_scan.h:180-191: out[i] = sum(in[0..i)) */
+int lcpp_scan_exclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in,
+                            void *out, uint64_t n, void *stream);
+/* replaces DeviceScan::InclusiveSum, device_scan.h:193-204: out[i] = sum(in[0..i]) */
+int lcpp_scan_inclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in,
+                            void *out, uint64_t n, void *stream);
+
+/* ---------------------------------------------------------------------
+ * DeviceRadixSort (onesweep, ascending, all key bits) — device/device_radix_sort.h
+ * Keys: any lcpp_dtype (signed and floating keys are bit-twiddled as in
+ * common/util_type.h:98-175; -0.0 and +0.0 compare equal).  Values: any
+ * lcpp_dtype (moved as raw 4- or 8-byte words).  n < 2^30.
+ * ------------------------------------------------------------------- */
+/* replaces DeviceRadixSort::GetSortKeysTempStorageBytes<K>(num_items), device_radix_sort.h:118-122 */
+int lcpp_radix_sort_keys_temp_bytes(lcpp_dtype k, uint64_t n, size_t *bytes);
+/* replaces DeviceRadixSort::SortKeys(cmdlist, temp, keys_in, keys_out, num_items),
+ * device_radix_sort.h:145-153 */
+int lcpp_radix_sort_keys(lcpp_dtype k, void *temp, size_t temp_bytes, const void *keys_in,
+                         void *keys_out, uint64_t n, void *stream);
+/* replaces DeviceRadixSort::GetSortPairsTempStorageBytes<K,V>(num_items), device_radix_sort.h:83-115 */
+int lcpp_radix_sort_pairs_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint64_t n, size_t *bytes);
+/* replaces DeviceRadixSort::SortPairs(cmdlist, temp, keys_in, keys_out, values_in,
+ * values_out, num_items), device_radix_sort.h:129-143.  Stable. */
+int lcpp_radix_sort_pairs(lcpp_dtype k, lcpp_dtype v, void *temp, size_t temp_bytes,
+                          const void *keys_in, void *keys_out, const void *vals_in,
+                          void *vals_out, uint64_t n, void *stream);
+
+/* ---------------------------------------------------------------------
+ * DeviceSegmentReduce — device/device_segment_reduce.h
+ * ------------------------------------------------------------------- */
+/* replaces DeviceSegmentReduce::GetTempStorageBytes<T>(num_item), device_segment_reduce.h:71-75
+ * (always 0) */
+int lcpp_segment_reduce_temp_bytes(lcpp_dtype t, uint64_t num_segments, size_t *bytes);
+/* replaces DeviceSegmentReduce::Sum(cmdlist, temp, d_in, d_out, num_segments, d_begin_offsets,
+ * d_end_offsets), device_segment_reduce.h:125-135:
+ * out[s] = 0 + sum(in[begin[s] .. end[s])); an empty segment (end <= begin) gives 0. */
+int lcpp_segment_reduce_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in,
+                            void *out, uint64_t num_segments, const uint32_t *begin,
+                            const uint32_t *end, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Instrumentation (no counterpart in the reference).  When enabled, every
+ * kernel launch made by the entry points above is bracketed by two HIP
+ * events recorded on the launch stream, so per-kernel device time can be
+ * read back.  Disabled by default; enabling it clears earlier records.
+ * ------------------------------------------------------------------- */
+int lcpp_profile_enable(int on);
+/* Synchronizes the recorded events and returns the number of distinct kernel names. */
+int lcpp_profile_count(void);
+/* Kernel i: name (truncated to name_cap), number of launches, summed duration in ms. */
+int lcpp_profile_get(int i, char *name, size_t name_cap, uint64_t *launches, double *total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LCPP_AMD_H */

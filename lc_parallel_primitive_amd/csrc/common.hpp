@@ -1,0 +1,196 @@
+// common.hpp — wave64 building blocks for the gfx950 (CDNA4) primitives.
+//
+// The reference builds everything on 32-lane warps (warp/details/*_shlf.h).
+// Here a wavefront is 64 lanes: reductions and scans take log2(64) = 6
+// steps, ballots are 64-bit masks and lane masks come from v_mbcnt.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <limits>
+#include <type_traits>
+
+#include "../../include/lcpp_amd.h"
+
+namespace lcpp {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- lanes
+__device__ __forceinline__ uint32_t lane_id()
+{
+    return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+// popcount(mask & lanes_below_me): rank of this lane among the lanes of `mask`.
+__device__ __forceinline__ uint32_t mask_rank(uint64_t mask)
+{
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// ---------------------------------------------------------------- ops
+struct SumOp {
+    template <class T>
+    __device__ __forceinline__ T operator()(T a, T b) const
+    {
+        if constexpr (std::is_integral_v<T>) {
+            using U = std::make_unsigned_t<T>;
+            return (T)((U)a + (U)b);  // two's-complement wraparound
+        } else {
+            return a + b;
+        }
+    }
+    template <class T>
+    static constexpr T identity() { return T(0); }
+};
+struct MinOp {
+    template <class T>
+    __device__ __forceinline__ T operator()(T a, T b) const { return b < a ? b : a; }
+    template <class T>
+    static constexpr T identity() { return std::numeric_limits<T>::max(); }
+};
+struct MaxOp {
+    template <class T>
+    __device__ __forceinline__ T operator()(T a, T b) const { return a < b ? b : a; }
+    template <class T>
+    static constexpr T identity() { return std::numeric_limits<T>::lowest(); }
+};
+
+// ---------------------------------------------------------------- shuffles
+template <class T>
+__device__ __forceinline__ T shfl_xor(T x, int m)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __shfl_xor(__builtin_bit_cast(int, x), m));
+    } else {
+        static_assert(sizeof(T) == 8, "4- or 8-byte types only");
+        int2 v = __builtin_bit_cast(int2, x);
+        v.x = __shfl_xor(v.x, m);
+        v.y = __shfl_xor(v.y, m);
+        return __builtin_bit_cast(T, v);
+    }
+}
+
+template <class T>
+__device__ __forceinline__ T shfl_up(T x, int d)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __shfl_up(__builtin_bit_cast(int, x), d));
+    } else {
+        int2 v = __builtin_bit_cast(int2, x);
+        v.x = __shfl_up(v.x, d);
+        v.y = __shfl_up(v.y, d);
+        return __builtin_bit_cast(T, v);
+    }
+}
+
+template <class T>
+__device__ __forceinline__ T read_lane(T x, int lane)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+    } else {
+        int2 v = __builtin_bit_cast(int2, x);
+        v.x = __builtin_amdgcn_readlane(v.x, lane);
+        v.y = __builtin_amdgcn_readlane(v.y, lane);
+        return __builtin_bit_cast(T, v);
+    }
+}
+
+// Butterfly all-reduce over the 64 lanes; every lane gets the result.
+template <class T, class Op>
+__device__ __forceinline__ T wave_allreduce(T x, Op op)
+{
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) x = op(x, shfl_xor(x, m));
+    return x;
+}
+
+// Kogge-Stone inclusive scan over the 64 lanes (lane order).
+template <class T, class Op>
+__device__ __forceinline__ T wave_inclusive_scan(T x, Op op)
+{
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        T y = shfl_up(x, d);
+        if (lane >= (uint32_t)d) x = op(y, x);
+    }
+    return x;
+}
+
+// ---------------------------------------------------------------- atomics
+// Device-coherent (agent scope) accesses: the 8 XCDs of an MI355X have
+// private L2s, so cross-workgroup publication must bypass them.
+template <class T>
+__device__ __forceinline__ T ld_relaxed(const T *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T ld_acquire(const T *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void st_relaxed(T *p, T v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void st_release(T *p, T v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ticket(uint32_t *ctr)
+{
+    return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- 16-byte vectors
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) 16-byte load/store: data touched once.
+__device__ __forceinline__ u32x4 ld16_nt(const void *p)
+{
+    return __builtin_nontemporal_load(static_cast<const u32x4 *>(p));
+}
+__device__ __forceinline__ void st16_nt(void *p, u32x4 v)
+{
+    __builtin_nontemporal_store(v, static_cast<u32x4 *>(p));
+}
+
+// ---------------------------------------------------------------- misc
+// Upper bound on the polls of one look-back wait (~1 s of s_sleep-paced
+// polling).  A wait that exceeds it gives up, so a kernel always drains even
+// if a predecessor's word were never published (the result is then wrong,
+// which the parity tests report, instead of a hung GPU).
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+__host__ __device__ constexpr uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+__host__ __device__ constexpr uint64_t align_up(uint64_t a, uint64_t b) { return ceil_div(a, b) * b; }
+
+// Host-side launch bookkeeping (profile.cpp): brackets a launch with HIP
+// events when instrumentation is enabled.
+struct LaunchScope {
+    LaunchScope(const char *name, hipStream_t s);
+    ~LaunchScope();
+    void *rec;
+};
+
+}  // namespace lcpp
+
+#define LCPP_LAUNCH(NAME, STREAM, ...)                       \
+    do {                                                      \
+        ::lcpp::LaunchScope lcpp_scope_(NAME, STREAM);        \
+        __VA_ARGS__;                                          \
+    } while (0)
+
+#define LCPP_CHECK_LAUNCH()                                   \
+    do {                                                      \
+        if (hipGetLastError() != hipSuccess) return LCPP_ERR_HIP; \
+    } while (0)

@@ -1,0 +1,140 @@
+// runtime.hip — status strings, version and launch instrumentation.
+//
+// Reference: runtime/core.h:35-112 (lazy JIT compile + memo, lcpp_check).
+// Here every kernel is compiled ahead of time for gfx950, so there is no JIT
+// cache; the C ABI returns status codes instead of asserting.
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace lcpp {
+namespace {
+
+struct Record {
+    std::string name;
+    hipEvent_t start, stop;
+};
+struct Aggregate {
+    std::string name;
+    uint64_t launches;
+    double total_ms;
+};
+
+std::mutex g_mu;
+bool g_on = false;
+std::vector<Record> g_pending;
+std::vector<Aggregate> g_agg;
+
+struct Open {
+    std::string name;
+    hipEvent_t start, stop;
+    hipStream_t stream;
+};
+
+}  // namespace
+
+LaunchScope::LaunchScope(const char *name, hipStream_t s) : rec(nullptr)
+{
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!g_on) return;
+    }
+    Open *o = new Open{name, nullptr, nullptr, s};
+    if (hipEventCreate(&o->start) != hipSuccess || hipEventCreate(&o->stop) != hipSuccess ||
+        hipEventRecord(o->start, s) != hipSuccess) {
+        delete o;
+        return;
+    }
+    rec = o;
+}
+
+LaunchScope::~LaunchScope()
+{
+    if (!rec) return;
+    Open *o = static_cast<Open *>(rec);
+    (void)hipEventRecord(o->stop, o->stream);
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_pending.push_back(Record{o->name, o->start, o->stop});
+    }
+    delete o;
+}
+
+}  // namespace lcpp
+
+using namespace lcpp;
+
+extern "C" int lcpp_version(void) { return LCPP_AMD_VERSION; }
+
+extern "C" const char *lcpp_status_string(int status)
+{
+    switch (status) {
+    case LCPP_OK: return "LCPP_OK";
+    case LCPP_ERR_INVALID_ARG: return "LCPP_ERR_INVALID_ARG";
+    case LCPP_ERR_TEMP_TOO_SMALL: return "LCPP_ERR_TEMP_TOO_SMALL";
+    case LCPP_ERR_UNSUPPORTED_DTYPE: return "LCPP_ERR_UNSUPPORTED_DTYPE";
+    case LCPP_ERR_HIP: return "LCPP_ERR_HIP";
+    default: return "LCPP_ERR_UNKNOWN";
+    }
+}
+
+static void drop_pending_locked()
+{
+    for (auto &r : g_pending) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    g_pending.clear();
+}
+
+extern "C" int lcpp_profile_enable(int on)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    drop_pending_locked();
+    g_agg.clear();
+    g_on = on != 0;
+    return LCPP_OK;
+}
+
+extern "C" int lcpp_profile_count(void)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = 0;
+    for (auto &r : g_pending) {
+        float ms = 0.f;
+        if (hipEventSynchronize(r.stop) != hipSuccess ||
+            hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) {
+            rc = LCPP_ERR_HIP;
+            continue;
+        }
+        bool found = false;
+        for (auto &a : g_agg)
+            if (a.name == r.name) {
+                a.launches += 1;
+                a.total_ms += ms;
+                found = true;
+                break;
+            }
+        if (!found) g_agg.push_back(Aggregate{r.name, 1, ms});
+    }
+    drop_pending_locked();
+    return rc ? rc : (int)g_agg.size();
+}
+
+extern "C" int lcpp_profile_get(int i, char *name, size_t name_cap, uint64_t *launches,
+                                double *total_ms)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (i < 0 || (size_t)i >= g_agg.size()) return LCPP_ERR_INVALID_ARG;
+    const Aggregate &a = g_agg[(size_t)i];
+    if (name && name_cap) {
+        size_t n = a.name.size() < name_cap - 1 ? a.name.size() : name_cap - 1;
+        a.name.copy(name, n);
+        name[n] = '\0';
+    }
+    if (launches) *launches = a.launches;
+    if (total_ms) *total_ms = a.total_ms;
+    return LCPP_OK;
+}

@@ -1,0 +1,131 @@
+"""Seeded synthetic inputs of the benchmark configurations, generated in HBM.
+
+Binding of liblcpp_datagen.so (csrc/datagen.hip).  Counter-based splitmix64:
+element i of every stream can be regenerated on the host, so the GPU tests
+can check full-size results without shipping inputs.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+lib_path = os.path.join(_PKG, "liblcpp_datagen.so")
+_lib = None
+
+# fixed stream seeds of the benchmark configurations
+SEED_REDUCE = 0xC1
+SEED_SCAN_U32 = 0xC2A
+SEED_SCAN_F32 = 0xC2B
+SEED_SORT_U32 = 0xC3A
+SEED_SORT_AND3 = (0xC3B1, 0xC3B2, 0xC3B3)
+SEED_PAIRS_U64 = 0xC4
+SEED_SEG_VALUES = 0xC5
+SEED_SEG_EMPTY = 0xC5E
+SEED_SEG_LEN = 0xC5F
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(lib_path):
+            raise FileNotFoundError(f"{lib_path} is missing: build with `python lc_parallel_primitive_amd/build.py`")
+        L = ctypes.CDLL(lib_path)
+        u64, vp, i = ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
+        for name in ("lcpp_gen_reduce_i32", "lcpp_gen_u8_u32", "lcpp_gen_normal_f32", "lcpp_gen_keys_u32",
+                     "lcpp_gen_keys_u64_low16"):
+            f = getattr(L, name)
+            f.restype, f.argtypes = i, [u64, u64, vp, vp]
+        L.lcpp_gen_keys_u32_and3.restype = i
+        L.lcpp_gen_keys_u32_and3.argtypes = [u64, u64, u64, u64, vp, vp]
+        L.lcpp_gen_iota_u32.restype = i
+        L.lcpp_gen_iota_u32.argtypes = [u64, vp, vp]
+        L.lcpp_gen_segments_host.restype = i
+        L.lcpp_gen_segments_host.argtypes = [u64, u64, u64, u64, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _run(rc: int, what: str):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc})")
+
+
+def reduce_i32(n: int, seed: int = SEED_REDUCE, device="cuda"):
+    """a_i = -1000 + floor(hi32(w_i) * 2001 / 2^32), uniform in [-1000, 1000]."""
+    import torch
+
+    t = torch.empty(n, dtype=torch.int32, device=device)
+    _run(lib().lcpp_gen_reduce_i32(seed, n, t.data_ptr(), _stream()), "gen_reduce_i32")
+    return t
+
+
+def u8_u32(n: int, seed: int = SEED_SCAN_U32, device="cuda"):
+    """x_i = hi32(w_i) >> 24, uniform in [0, 255]."""
+    import torch
+
+    t = torch.empty(n, dtype=torch.uint32, device=device)
+    _run(lib().lcpp_gen_u8_u32(seed, n, t.data_ptr(), _stream()), "gen_u8_u32")
+    return t
+
+
+def normal_f32(n: int, seed: int = SEED_SCAN_F32, device="cuda"):
+    """Box-Muller (cos branch) in double, cast to float32."""
+    import torch
+
+    t = torch.empty(n, dtype=torch.float32, device=device)
+    _run(lib().lcpp_gen_normal_f32(seed, n, t.data_ptr(), _stream()), "gen_normal_f32")
+    return t
+
+
+def keys_u32(n: int, seed: int = SEED_SORT_U32, device="cuda"):
+    """k_i = lo32(w_i): uniform over the full 32-bit range."""
+    import torch
+
+    t = torch.empty(n, dtype=torch.uint32, device=device)
+    _run(lib().lcpp_gen_keys_u32(seed, n, t.data_ptr(), _stream()), "gen_keys_u32")
+    return t
+
+
+def keys_u32_and3(n: int, seeds=SEED_SORT_AND3, device="cuda"):
+    """k_i = lo32(wA_i) & lo32(wB_i) & lo32(wC_i): each bit set with p = 1/8."""
+    import torch
+
+    t = torch.empty(n, dtype=torch.uint32, device=device)
+    _run(lib().lcpp_gen_keys_u32_and3(seeds[0], seeds[1], seeds[2], n, t.data_ptr(), _stream()), "gen_and3")
+    return t
+
+
+def keys_u64_low16(n: int, seed: int = SEED_PAIRS_U64, device="cuda"):
+    """k_i = w_i & 0xFFFF (upper 48 bits zero)."""
+    import torch
+
+    t = torch.empty(n, dtype=torch.uint64, device=device)
+    _run(lib().lcpp_gen_keys_u64_low16(seed, n, t.data_ptr(), _stream()), "gen_keys_u64_low16")
+    return t
+
+
+def iota_u32(n: int, device="cuda"):
+    import torch
+
+    t = torch.empty(n, dtype=torch.uint32, device=device)
+    _run(lib().lcpp_gen_iota_u32(n, t.data_ptr(), _stream()), "gen_iota_u32")
+    return t
+
+
+def segments(n_items: int, n_segments: int, seed_empty: int = SEED_SEG_EMPTY, seed_len: int = SEED_SEG_LEN):
+    """CSR begin/end offsets (numpy uint32, host): 5 % empty, geometric lengths
+    of mean 128/0.95 otherwise, rescaled to cover exactly n_items."""
+    import numpy as np
+
+    b = np.empty(n_segments, dtype=np.uint32)
+    e = np.empty(n_segments, dtype=np.uint32)
+    _run(lib().lcpp_gen_segments_host(seed_empty, seed_len, n_items, n_segments, b.ctypes.data, e.ctypes.data),
+         "gen_segments_host")
+    return b, e

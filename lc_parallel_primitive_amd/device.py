@@ -1,0 +1,191 @@
+"""Device-level primitives with the reference's class and method names.
+
+Mirrors src/lcpp/device/device_{reduce,scan,radix_sort,segment_reduce}.h of
+the reference: caller-owned temp storage sized by the static
+Get*TempStorageBytes queries, then an asynchronous call on a stream.  The
+reference records into an LC CommandList; here the work is enqueued on a
+HIP stream (default: torch's current stream).  Buffers are device tensors
+(torch here; anything with .data_ptr(), .numel(), .element_size(), .dtype).
+
+Differences from the reference, by design:
+  * errors raise LcppError (the reference asserts in debug builds and
+    ignores failures in release, runtime/core.h:56-67);
+  * sizes are checked against the buffers before any launch;
+  * DeviceReduce.Max starts from numeric lowest() (the reference uses
+    numeric_limits<T>::min(), wrong for floating point,
+    device_reduce.h:181-185).
+"""
+from __future__ import annotations
+
+import ctypes
+
+from ._capi import check, dtype_code, lib
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return ctypes.c_void_p(stream)
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _nbytes(t) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
+
+
+def _need(t, n: int, what: str):
+    if n > 0 and (t is None or t.numel() < n):
+        raise ValueError(f"{what}: buffer holds {0 if t is None else t.numel()} elements, need {n}")
+
+
+def _same_dtype(a, b, what: str):
+    if a.dtype != b.dtype:
+        raise TypeError(f"{what}: dtype mismatch {a.dtype} vs {b.dtype}")
+
+
+def _query(fn, *args) -> int:
+    out = ctypes.c_size_t()
+    check(fn(*args, ctypes.byref(out)), fn.__name__)
+    return out.value
+
+
+class DeviceReduce:
+    """device/device_reduce.h:37-185 (Sum / Min / Max)."""
+
+    def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
+        # geometry is fixed per dtype inside the library (tuned for gfx950);
+        # the arguments are accepted for source compatibility
+        self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
+
+    def create(self, device=None, debug_stream=None):
+        return self
+
+    @staticmethod
+    def GetTempStorageBytes(dtype, num_item: int) -> int:
+        return _query(lib().lcpp_reduce_temp_bytes, dtype_code(dtype), num_item)
+
+    def _run(self, fn, temp, d_in, d_out, num_item, stream):
+        _need(d_in, num_item, "d_in")
+        _need(d_out, 1, "d_out")
+        _same_dtype(d_in, d_out, fn.__name__)
+        check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), num_item,
+                 _stream(stream)), fn.__name__)
+
+    def Sum(self, temp_storage, d_in, d_out, num_item: int, stream=None):
+        self._run(lib().lcpp_reduce_sum, temp_storage, d_in, d_out, num_item, stream)
+
+    def Min(self, temp_storage, d_in, d_out, num_item: int, stream=None):
+        self._run(lib().lcpp_reduce_min, temp_storage, d_in, d_out, num_item, stream)
+
+    def Max(self, temp_storage, d_in, d_out, num_item: int, stream=None):
+        self._run(lib().lcpp_reduce_max, temp_storage, d_in, d_out, num_item, stream)
+
+
+class DeviceScan:
+    """device/device_scan.h:33-204 (ExclusiveSum / InclusiveSum)."""
+
+    def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
+        self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
+
+    def create(self, device=None, debug_stream=None):
+        return self
+
+    @staticmethod
+    def GetTempStorageBytes(dtype, num_items: int) -> int:
+        return _query(lib().lcpp_scan_temp_bytes, dtype_code(dtype), num_items)
+
+    def _run(self, fn, temp, d_in, d_out, num_items, stream):
+        _need(d_in, num_items, "d_in")
+        _need(d_out, num_items, "d_out")
+        _same_dtype(d_in, d_out, fn.__name__)
+        check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), num_items,
+                 _stream(stream)), fn.__name__)
+
+    def ExclusiveSum(self, temp_storage, d_in, d_out, num_items: int, stream=None):
+        self._run(lib().lcpp_scan_exclusive_sum, temp_storage, d_in, d_out, num_items, stream)
+
+    def InclusiveSum(self, temp_storage, d_in, d_out, num_items: int, stream=None):
+        self._run(lib().lcpp_scan_inclusive_sum, temp_storage, d_in, d_out, num_items, stream)
+
+
+class DeviceRadixSort:
+    """device/device_radix_sort.h:37-153 (onesweep SortKeys / SortPairs, ascending)."""
+
+    def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
+        self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
+
+    def create(self, device=None, debug_stream=None):
+        return self
+
+    @staticmethod
+    def GetSortKeysTempStorageBytes(key_dtype, num_items: int) -> int:
+        return _query(lib().lcpp_radix_sort_keys_temp_bytes, dtype_code(key_dtype), num_items)
+
+    @staticmethod
+    def GetSortPairsTempStorageBytes(key_dtype, value_dtype, num_items: int) -> int:
+        return _query(lib().lcpp_radix_sort_pairs_temp_bytes, dtype_code(key_dtype), dtype_code(value_dtype),
+                      num_items)
+
+    def SortKeys(self, temp_storage, d_keys_in, d_keys_out, num_items: int, stream=None):
+        _need(d_keys_in, num_items, "d_keys_in")
+        _need(d_keys_out, num_items, "d_keys_out")
+        _same_dtype(d_keys_in, d_keys_out, "SortKeys")
+        L = lib()
+        check(L.lcpp_radix_sort_keys(dtype_code(d_keys_in.dtype), _ptr(temp_storage), _nbytes(temp_storage),
+                                     _ptr(d_keys_in), _ptr(d_keys_out), num_items, _stream(stream)),
+              "lcpp_radix_sort_keys")
+
+    def SortPairs(self, temp_storage, d_keys_in, d_keys_out, d_values_in, d_values_out, num_items: int,
+                  stream=None):
+        for t, nm in ((d_keys_in, "d_keys_in"), (d_keys_out, "d_keys_out"), (d_values_in, "d_values_in"),
+                      (d_values_out, "d_values_out")):
+            _need(t, num_items, nm)
+        _same_dtype(d_keys_in, d_keys_out, "SortPairs keys")
+        _same_dtype(d_values_in, d_values_out, "SortPairs values")
+        L = lib()
+        check(L.lcpp_radix_sort_pairs(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype),
+                                      _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_keys_in),
+                                      _ptr(d_keys_out), _ptr(d_values_in), _ptr(d_values_out), num_items,
+                                      _stream(stream)),
+              "lcpp_radix_sort_pairs")
+
+
+class DeviceSegmentReduce:
+    """device/device_segment_reduce.h:26-135 (Sum with CSR begin/end offsets)."""
+
+    def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
+        self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
+
+    def create(self, device=None, debug_stream=None):
+        return self
+
+    @staticmethod
+    def GetTempStorageBytes(dtype, num_segments: int = 0) -> int:
+        return _query(lib().lcpp_segment_reduce_temp_bytes, dtype_code(dtype), num_segments)
+
+    def Sum(self, temp_storage, d_in, d_out, num_segments: int, d_begin_offsets, d_end_offsets, stream=None):
+        _need(d_out, num_segments, "d_out")
+        _need(d_begin_offsets, num_segments, "d_begin_offsets")
+        _need(d_end_offsets, num_segments, "d_end_offsets")
+        _same_dtype(d_in, d_out, "Sum")
+        if num_segments:
+            import torch
+
+            # every segment must lie inside d_in (checked on the host, no GPU fault on bad offsets)
+            b = d_begin_offsets[:num_segments].to(torch.int64)
+            e = d_end_offsets[:num_segments].to(torch.int64)
+            hi = torch.where(e > b, e, torch.zeros_like(e)).max().item()
+            if hi > d_in.numel():
+                raise ValueError(f"segment end {hi} exceeds d_in ({d_in.numel()} elements)")
+        L = lib()
+        check(L.lcpp_segment_reduce_sum(dtype_code(d_in.dtype), _ptr(temp_storage), _nbytes(temp_storage),
+                                        _ptr(d_in), _ptr(d_out), num_segments, _ptr(d_begin_offsets),
+                                        _ptr(d_end_offsets), _stream(stream)),
+              "lcpp_segment_reduce_sum")

@@ -1,0 +1,222 @@
+"""numpy binding of the CPU oracle (oracle/lcpp_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() (as
+the checker) and bench.py's cpu_baseline leg.  The shipped library never
+imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+lib_path = os.path.join(_DIR, "liblcpp_oracle.so")
+_lib = None
+
+I32, U32, F32, I64, U64, F64 = range(6)
+OP_SUM, OP_MIN, OP_MAX = range(3)
+_NP_CODE = {
+    np.dtype(np.int32): I32,
+    np.dtype(np.uint32): U32,
+    np.dtype(np.float32): F32,
+    np.dtype(np.int64): I64,
+    np.dtype(np.uint64): U64,
+    np.dtype(np.float64): F64,
+}
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _DIR], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(lib_path):
+            build()
+        L = ctypes.CDLL(lib_path)
+        vp, u64, i, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_uint32
+        sig = {
+            "lcor_splitmix64_next": (u64, [ctypes.POINTER(u64)]),
+            "lcor_word": (u64, [u64, u64]),
+            "lcor_gen_words": (None, [u64, u64, u64, vp]),
+            "lcor_gen_reduce_i32": (None, [u64, u64, vp]),
+            "lcor_gen_u8_u32": (None, [u64, u64, vp]),
+            "lcor_gen_normal_f32": (None, [u64, u64, vp]),
+            "lcor_gen_keys_u32": (None, [u64, u64, vp]),
+            "lcor_gen_keys_u32_and3": (None, [u64, u64, u64, u64, vp]),
+            "lcor_gen_keys_u64_low16": (None, [u64, u64, vp]),
+            "lcor_gen_iota_u32": (None, [u64, vp]),
+            "lcor_gen_segments": (i, [u64, u64, u64, u64, vp, vp]),
+            "lcor_reduce": (i, [i, i, vp, u64, vp]),
+            "lcor_reduce_f64": (i, [i, vp, u64, vp, vp]),
+            "lcor_reduce_mt": (i, [i, i, vp, u64, vp, i]),
+            "lcor_scan": (i, [i, i, vp, vp, u64]),
+            "lcor_scan_f64": (i, [i, i, vp, vp, vp, u64]),
+            "lcor_scan_mt": (i, [i, i, vp, vp, u64, i]),
+            "lcor_lookback_kat": (i, [u32, i, vp, vp]),
+            "lcor_radix_sort": (i, [i, i, vp, vp, vp, vp, u64, i, i, u32]),
+            "lcor_check_stable_pairs_u64_u32": (i, [vp, vp, vp, u64]),
+            "lcor_check_sorted_permutation_u32": (i, [vp, vp, u64]),
+            "lcor_segment_reduce": (i, [i, i, vp, vp, u64, vp, vp]),
+            "lcor_segment_reduce_f64": (i, [i, vp, u64, vp, vp, vp, vp]),
+            "lcor_segment_reduce_mt": (i, [i, vp, vp, u64, vp, vp, i]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _code(a: np.ndarray) -> int:
+    return _NP_CODE[a.dtype]
+
+
+def _ok(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"oracle {what} failed ({rc})")
+
+
+# ---------------------------------------------------------------- generators
+def word(seed: int, i: int) -> int:
+    return lib().lcor_word(seed, i)
+
+
+def words(seed: int, n: int, start: int = 0) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    lib().lcor_gen_words(seed, start, n, _p(out))
+    return out
+
+
+def gen(kind: str, n: int, *seeds) -> np.ndarray:
+    L = lib()
+    if kind == "reduce_i32":
+        out = np.empty(n, np.int32); L.lcor_gen_reduce_i32(seeds[0], n, _p(out))
+    elif kind == "u8_u32":
+        out = np.empty(n, np.uint32); L.lcor_gen_u8_u32(seeds[0], n, _p(out))
+    elif kind == "normal_f32":
+        out = np.empty(n, np.float32); L.lcor_gen_normal_f32(seeds[0], n, _p(out))
+    elif kind == "keys_u32":
+        out = np.empty(n, np.uint32); L.lcor_gen_keys_u32(seeds[0], n, _p(out))
+    elif kind == "keys_u32_and3":
+        out = np.empty(n, np.uint32); L.lcor_gen_keys_u32_and3(seeds[0], seeds[1], seeds[2], n, _p(out))
+    elif kind == "keys_u64_low16":
+        out = np.empty(n, np.uint64); L.lcor_gen_keys_u64_low16(seeds[0], n, _p(out))
+    elif kind == "iota_u32":
+        out = np.empty(n, np.uint32); L.lcor_gen_iota_u32(n, _p(out))
+    else:
+        raise ValueError(kind)
+    return out
+
+
+def segments(seed_empty: int, seed_len: int, n_items: int, n_segments: int):
+    b = np.empty(n_segments, np.uint32)
+    e = np.empty(n_segments, np.uint32)
+    _ok(lib().lcor_gen_segments(seed_empty, seed_len, n_items, n_segments, _p(b), _p(e)), "gen_segments")
+    return b, e
+
+
+# ---------------------------------------------------------------- reduce
+def reduce(op: int, a: np.ndarray, nthreads: int = 1):
+    a = np.ascontiguousarray(a)
+    out = np.zeros(1, a.dtype)
+    if nthreads == 1:
+        _ok(lib().lcor_reduce(op, _code(a), _p(a), a.size, _p(out)), "reduce")
+    else:
+        _ok(lib().lcor_reduce_mt(op, _code(a), _p(a), a.size, _p(out), nthreads), "reduce_mt")
+    return out[0]
+
+
+def reduce_f64(a: np.ndarray):
+    """(double-precision sum, sum of |x|)."""
+    a = np.ascontiguousarray(a)
+    s = np.zeros(1, np.float64)
+    ab = np.zeros(1, np.float64)
+    _ok(lib().lcor_reduce_f64(_code(a), _p(a), a.size, _p(s), _p(ab)), "reduce_f64")
+    return float(s[0]), float(ab[0])
+
+
+# ---------------------------------------------------------------- scan
+def scan(a: np.ndarray, inclusive: bool, nthreads: int = 1) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.empty_like(a)
+    if nthreads == 1:
+        _ok(lib().lcor_scan(int(inclusive), _code(a), _p(a), _p(out), a.size), "scan")
+    else:
+        _ok(lib().lcor_scan_mt(int(inclusive), _code(a), _p(a), _p(out), a.size, nthreads), "scan_mt")
+    return out
+
+
+def scan_f64(a: np.ndarray, inclusive: bool):
+    """(double-precision prefix sums, prefix sums of |x|)."""
+    a = np.ascontiguousarray(a)
+    out = np.empty(a.size, np.float64)
+    ab = np.empty(a.size, np.float64)
+    _ok(lib().lcor_scan_f64(int(inclusive), _code(a), _p(a), _p(out), _p(ab), a.size), "scan_f64")
+    return out, ab
+
+
+def lookback_kat(num_tiles: int, nthreads: int):
+    ex = np.empty(num_tiles, np.int32)
+    inc = np.empty(num_tiles, np.int32)
+    _ok(lib().lcor_lookback_kat(num_tiles, nthreads, _p(ex), _p(inc)), "lookback_kat")
+    return ex, inc
+
+
+# ---------------------------------------------------------------- sort
+def radix_sort(keys: np.ndarray, values: np.ndarray | None = None, descending: bool = False, nthreads: int = 1,
+               tile_items: int = 4096):
+    keys = np.ascontiguousarray(keys)
+    kout = np.empty_like(keys)
+    vb = 0
+    vout = None
+    if values is not None:
+        values = np.ascontiguousarray(values)
+        vout = np.empty_like(values)
+        vb = values.itemsize
+    _ok(lib().lcor_radix_sort(_code(keys), vb, _p(keys), _p(kout),
+                              _p(values) if values is not None else None,
+                              _p(vout) if vout is not None else None,
+                              keys.size, int(descending), nthreads, tile_items), "radix_sort")
+    return (kout, vout) if values is not None else kout
+
+
+def check_stable_pairs_u64_u32(keys_in, keys_out, vals_out) -> bool:
+    return lib().lcor_check_stable_pairs_u64_u32(_p(keys_in), _p(keys_out), _p(vals_out), keys_in.size) == 1
+
+
+def check_sorted_permutation_u32(keys_in, keys_out) -> bool:
+    return lib().lcor_check_sorted_permutation_u32(_p(keys_in), _p(keys_out), keys_in.size) == 1
+
+
+# ---------------------------------------------------------------- segment reduce
+def segment_reduce(op: int, a: np.ndarray, begin: np.ndarray, end: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    out = np.empty(begin.size, a.dtype)
+    _ok(lib().lcor_segment_reduce(op, _code(a), _p(a), _p(out), begin.size, _p(begin), _p(end)), "segment_reduce")
+    return out
+
+
+def segment_reduce_f64(a: np.ndarray, begin: np.ndarray, end: np.ndarray):
+    a = np.ascontiguousarray(a)
+    s = np.empty(begin.size, np.float64)
+    ab = np.empty(begin.size, np.float64)
+    _ok(lib().lcor_segment_reduce_f64(_code(a), _p(a), begin.size, _p(begin), _p(end), _p(s), _p(ab)),
+        "segment_reduce_f64")
+    return s, ab
+
+
+def segment_reduce_mt(a: np.ndarray, begin: np.ndarray, end: np.ndarray, nthreads: int) -> np.ndarray:
+    out = np.empty(begin.size, a.dtype)
+    _ok(lib().lcor_segment_reduce_mt(_code(a), _p(a), _p(out), begin.size, _p(begin), _p(end), nthreads),
+        "segment_reduce_mt")
+    return out

@@ -1,0 +1,122 @@
+"""CPU-side checks of the C ABI boundary: the HIP library loads without a GPU,
+exports every symbol include/lcpp_amd.h declares, its size queries are pure
+host arithmetic, and argument validation rejects bad calls before any launch."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "lcpp_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lcpp_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    import lc_parallel_primitive_amd as lcpp
+
+    return lcpp.lib()
+
+
+def test_every_declared_symbol_is_exported(L):
+    names = declared_functions()
+    assert len(names) >= 18
+    out = subprocess.run(["nm", "-D", "--defined-only", L._name], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (lcpp_[a-z0-9_]+)$", out, flags=re.M))
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    for n in names:  # and ctypes resolves them
+        getattr(L, n)
+
+
+def test_bindings_cover_header():
+    from lc_parallel_primitive_amd._capi import SIGNATURES
+
+    assert set(SIGNATURES) == set(declared_functions())
+
+
+def test_version_and_status_strings(L):
+    assert L.lcpp_version() == 100
+    assert L.lcpp_status_string(0) == b"LCPP_OK"
+    assert L.lcpp_status_string(-2) == b"LCPP_ERR_TEMP_TOO_SMALL"
+    assert L.lcpp_status_string(-99) == b"LCPP_ERR_UNKNOWN"
+
+
+def _q(fn, *args):
+    out = ctypes.c_size_t(12345)
+    rc = fn(*args, ctypes.byref(out))
+    return rc, out.value
+
+
+def test_temp_bytes_queries(L):
+    # reduce: one partial per workgroup (<= 2048), none when one workgroup suffices
+    assert _q(L.lcpp_reduce_temp_bytes, 0, 0) == (0, 0)
+    assert _q(L.lcpp_reduce_temp_bytes, 0, 8192) == (0, 0)
+    rc, b = _q(L.lcpp_reduce_temp_bytes, 0, 1 << 28)
+    assert rc == 0 and b == 2048 * 4
+    rc, b = _q(L.lcpp_reduce_temp_bytes, 5, 1 << 28)
+    assert rc == 0 and b == 2048 * 8
+    # scan: ticket + one packed 64-bit word per 4096-element tile
+    rc, b = _q(L.lcpp_scan_temp_bytes, 1, 1 << 28)
+    assert rc == 0 and b == 256 + (1 << 16) * 8
+    # sort: bins + tickets + 2 look-back regions + key scratch (no value scratch)
+    rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, 1 << 28)
+    tiles = (1 << 28) // 4096
+    assert rc == 0 and b == 4 * 256 * 4 + 256 + 2 * tiles * 256 * 4 + (1 << 28) * 4
+    rc, bp = _q(L.lcpp_radix_sort_pairs_temp_bytes, 4, 1, 1 << 27)
+    assert rc == 0 and bp > (1 << 27) * 12
+    # segment reduce needs none (as the reference)
+    assert _q(L.lcpp_segment_reduce_temp_bytes, 2, 1 << 20) == (0, 0)
+
+
+def test_unsupported_dtype_and_null_args(L):
+    assert _q(L.lcpp_reduce_temp_bytes, 17, 10)[0] == -3
+    assert L.lcpp_reduce_temp_bytes(0, 10, None) == -1
+    # argument errors are detected before any HIP call (no GPU here)
+    assert L.lcpp_reduce_sum(9, None, 0, None, None, 10, None) == -3
+    assert L.lcpp_reduce_sum(0, None, 0, None, None, 10, None) == -1
+    assert L.lcpp_scan_exclusive_sum(0, None, 0, None, None, 10, None) == -1
+    assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 10, None) == -1
+    assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 1 << 30, None) == -1  # n >= 2^30
+    assert L.lcpp_segment_reduce_sum(2, None, 0, None, None, 10, None, None, None) == -1
+    # zero-sized work is a no-op success
+    assert L.lcpp_scan_inclusive_sum(0, None, 0, None, None, 0, None) == 0
+    assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 0, None) == 0
+    assert L.lcpp_segment_reduce_sum(2, None, 0, None, None, 0, None, None, None) == 0
+
+
+def test_temp_too_small_detected_before_launch(L):
+    dummy = ctypes.c_void_p(0x1000)
+    assert L.lcpp_scan_exclusive_sum(1, dummy, 16, dummy, dummy, 1 << 20, None) == -2
+    assert L.lcpp_radix_sort_keys(1, dummy, 16, dummy, dummy, 1 << 20, None) == -2
+    assert L.lcpp_reduce_sum(0, dummy, 16, dummy, dummy, 1 << 28, None) == -2
+
+
+def test_misaligned_temp_rejected(L):
+    p = ctypes.c_void_p(0x1000 + 4)
+    _, b = _q(L.lcpp_scan_temp_bytes, 1, 1 << 20)
+    assert L.lcpp_scan_exclusive_sum(1, p, b, p, p, 1 << 20, None) == -1
+
+
+def test_cpp_host_api_compiles():
+    """include/lcpp/parallel_primitive.h (the reference's class names over the
+    C ABI) is valid C++17 on its own."""
+    src = '#include "lcpp/parallel_primitive.h"\nint main(){return 0;}\n'
+    r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                        "-x", "c++", "-"], input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_c_header_is_plain_c():
+    src = '#include "lcpp_amd.h"\nint main(void){return lcpp_version();}\n'
+    r = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                        "-x", "c", "-"], input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

@@ -1,0 +1,26 @@
+"""The device-side input generators equal the oracle's host restatement."""
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def test_generators_match_host(gpu):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen as dg
+
+    n = 100_003
+    assert (g.to_host(dg.reduce_i32(n)) == o.gen("reduce_i32", n, dg.SEED_REDUCE)).all()
+    assert (g.to_host(dg.u8_u32(n)) == o.gen("u8_u32", n, dg.SEED_SCAN_U32)).all()
+    assert (g.to_host(dg.keys_u32(n)) == o.gen("keys_u32", n, dg.SEED_SORT_U32)).all()
+    assert (g.to_host(dg.keys_u32_and3(n)) == o.gen("keys_u32_and3", n, *dg.SEED_SORT_AND3)).all()
+    assert (g.to_host(dg.keys_u64_low16(n)) == o.gen("keys_u64_low16", n, dg.SEED_PAIRS_U64)).all()
+    assert (g.to_host(dg.iota_u32(n)) == np.arange(n, dtype=np.uint32)).all()
+    # Box-Muller in double through the device libm: equal after rounding to float32
+    # except for rare last-ulp differences of log/cos
+    dev = g.to_host(dg.normal_f32(n))
+    host = o.gen("normal_f32", n, dg.SEED_SCAN_F32)
+    ulps = np.abs(dev.view(np.int32).astype(np.int64) - host.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.999

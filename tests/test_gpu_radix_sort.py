@@ -1,0 +1,140 @@
+"""DeviceRadixSort::SortKeys/SortPairs (onesweep) on the GPU through the C ABI.
+Bit-exact against the oracle (itself pinned against numpy stable sorts and
+the reference's known answers); pairs are checked for stability; full-size
+configurations use O(N) sortedness + multiset / stability checkers."""
+import numpy as np
+import pytest
+
+from conftest import golden, log
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+KEY_DTYPES = [np.uint32, np.int32, np.float32, np.uint64, np.int64, np.float64]
+SIZES = [1, 2, 63, 64, 65, 4095, 4096, 4097, 8191, 100_003]
+
+
+def sort_keys(d_in, n, dtype, pad=0):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceRadixSort
+
+    out = g.empty(n, dtype, pad=pad)
+    tmp = g.temp(DeviceRadixSort.GetSortKeysTempStorageBytes(np.dtype(dtype).name, n))
+    DeviceRadixSort().SortKeys(tmp, d_in, out, n)
+    return out
+
+
+def sort_pairs(dk, dv, n, kdt, vdt):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceRadixSort
+
+    ko = g.empty(n, kdt)
+    vo = g.empty(n, vdt)
+    tmp = g.temp(DeviceRadixSort.GetSortPairsTempStorageBytes(np.dtype(kdt).name, np.dtype(vdt).name, n))
+    DeviceRadixSort().SortPairs(tmp, dk, ko, dv, vo, n)
+    return ko, vo
+
+
+def same_bits(a, b):
+    return a.tobytes() == b.tobytes()
+
+
+def test_kat_reversed_keys(gpu):
+    # device_radix_sort_one_sweep.cpp:120-151: keys N-1..0, N = 2^0..2^23
+    import gpu_util as g
+
+    for k in range(24):
+        n = 1 << k
+        log(f"sort reversed n={n}")
+        a = np.arange(n - 1, -1, -1, dtype=np.uint32)
+        got = g.to_host(sort_keys(g.to_dev(a), n, np.uint32))
+        assert (got == np.arange(n, dtype=np.uint32)).all()
+
+
+@pytest.mark.parametrize("n", [32, 256, 4096])
+def test_kat_float_keys_golden(gpu, n):
+    # device_radix_sort_one_sweep.cpp:61-118 (ascending half; descending is not part of this build)
+    import gpu_util as g
+
+    a = golden(f"sort_float_{n}_asc_in_f32.bin", np.float32)
+    got = g.to_host(sort_keys(g.to_dev(a), n, np.float32))
+    assert same_bits(got, golden(f"sort_float_{n}_asc_expect_f32.bin", np.float32))
+
+
+def test_kat_pairs_golden(gpu):
+    # device_radix_sort_one_sweep.cpp:153-279 procedure (uint keys, float values)
+    import gpu_util as g
+
+    k = golden("sort_pairs_16384_keys_in_u32.bin", np.uint32)
+    v = golden("sort_pairs_16384_vals_in_f32.bin", np.float32)
+    ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), k.size, np.uint32, np.float32)
+    assert same_bits(g.to_host(ko), golden("sort_pairs_16384_keys_expect_u32.bin", np.uint32))
+    assert same_bits(g.to_host(vo), golden("sort_pairs_16384_vals_expect_f32.bin", np.float32))
+
+
+@pytest.mark.parametrize("dtype", KEY_DTYPES)
+@pytest.mark.parametrize("n", SIZES)
+def test_keys_vs_oracle(gpu, dtype, n):
+    import gpu_util as g
+
+    a = g.random_array(dtype, n, seed=n)
+    log(f"sort keys {np.dtype(dtype).name} n={n}")
+    d = g.to_dev(a)
+    got = g.to_host(sort_keys(d, n, dtype))
+    assert same_bits(got, o.radix_sort(a))  # bit-exact, including the order of -0.0 / +0.0
+    assert same_bits(g.to_host(d), a)  # input preserved
+
+
+@pytest.mark.parametrize("kdt,vdt", [(np.uint32, np.uint32), (np.uint64, np.uint32), (np.int32, np.float64),
+                                     (np.float64, np.int64), (np.float32, np.uint32)])
+@pytest.mark.parametrize("n", [1, 4097, 100_003])
+def test_pairs_stable_vs_oracle(gpu, kdt, vdt, n):
+    import gpu_util as g
+
+    k = g.random_array(kdt, n, seed=3)
+    if np.dtype(kdt).kind in "iu":
+        k = k & np.array(0xFF, dtype=kdt)  # heavy duplication: stability matters
+    v = np.arange(n, dtype=vdt)
+    log(f"sort pairs {np.dtype(kdt).name}/{np.dtype(vdt).name} n={n}")
+    ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, kdt, vdt)
+    rk, rv = o.radix_sort(k, v)
+    assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
+
+
+def test_low_entropy_keys(gpu):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 3_000_017
+    d = datagen.keys_u32_and3(n)
+    got = g.to_host(sort_keys(d, n, np.uint32))
+    h = g.to_host(d)
+    assert same_bits(got, o.radix_sort(h, nthreads=8))
+    assert (h[:1000] == o.gen("keys_u32_and3", 1000, *datagen.SEED_SORT_AND3)).all()
+
+
+@pytest.mark.parametrize("which", ["uniform", "and3"])
+def test_full_size_u32(gpu, which):
+    # BASELINE config C3a/C3b: 2^28 uint32 keys
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    log(f"sort keys u32 full 2^28 {which}")
+    d = datagen.keys_u32(n) if which == "uniform" else datagen.keys_u32_and3(n)
+    got = g.to_host(sort_keys(d, n, np.uint32))
+    h = g.to_host(d)
+    assert o.check_sorted_permutation_u32(h, got)
+
+
+def test_full_size_pairs_u64_index(gpu):
+    # 2^27 uint64 keys with 16 random low bits, values = index
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 27
+    log("sort pairs u64/u32 full 2^27")
+    k = datagen.keys_u64_low16(n)
+    v = datagen.iota_u32(n)
+    ko, vo = sort_pairs(k, v, n, np.uint64, np.uint32)
+    assert o.check_stable_pairs_u64_u32(g.to_host(k), g.to_host(ko), g.to_host(vo))

@@ -1,0 +1,120 @@
+"""DeviceReduce::Sum/Min/Max on the GPU through the C ABI, against the oracle
+(bit-exact for integers; float sums within |err| <= 1e-5 * sum|x| of a
+float64 reduction)."""
+import numpy as np
+import pytest
+
+from conftest import golden, log
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+RTOL_SUM = 1e-5  # normwise: |err| <= RTOL_SUM * sum(|x|)
+DTYPES = [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64]
+
+
+def run(op, a_dev, n, dtype):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce
+
+    r = DeviceReduce()
+    out = g.empty(1, dtype)
+    tmp = g.temp(DeviceReduce.GetTempStorageBytes(np.dtype(dtype).name, n))
+    getattr(r, op)(tmp, a_dev, out, n)
+    return g.to_host(out)[0]
+
+
+def test_kat_sum_of_ones(gpu):
+    # device_reduce_test.cpp:66-90: Sum<uint> of N ones == N, N = 2^k + 1, k < 24
+    import gpu_util as g
+
+    for k in range(24):
+        n = (1 << k) + 1
+        log(f"reduce ones n={n}")
+        assert run("Sum", g.to_dev(np.ones(n, np.uint32)), n, np.uint32) == n
+
+
+def test_kat_min_max_shuffled(gpu):
+    # device_reduce_test.cpp:120-166
+    import gpu_util as g
+
+    a = golden("reduce_shuffled_4096_i32.bin", np.int32)
+    exp = golden("reduce_shuffled_4096_expect_min_max_sum_i32.bin", np.int32)
+    d = g.to_dev(a)
+    assert run("Min", d, a.size, np.int32) == exp[0]
+    assert run("Max", d, a.size, np.int32) == exp[1]
+    assert run("Sum", d, a.size, np.int32) == exp[2]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 63, 4097, 32768, 1_000_003])
+@pytest.mark.parametrize("pad", [0, 1])
+def test_all_dtypes_vs_oracle(gpu, dtype, n, pad):
+    import gpu_util as g
+
+    a = g.random_array(dtype, n, seed=n)
+    log(f"reduce {np.dtype(dtype).name} n={n} pad={pad}")
+    d = g.to_dev(a, pad=pad)
+    for op, code in (("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        assert run(op, d, n, dtype) == o.reduce(code, a)
+    got = run("Sum", d, n, dtype)
+    if np.dtype(dtype).kind == "f":
+        s, ab = o.reduce_f64(a)
+        assert abs(float(got) - s) <= RTOL_SUM * ab + 1e-30
+    else:
+        assert got == o.reduce(o.OP_SUM, a)
+
+
+def test_empty_gives_init(gpu):
+    import gpu_util as g
+
+    d = g.empty(4, np.int32)
+    assert run("Sum", d, 0, np.int32) == 0
+    assert run("Min", d, 0, np.int32) == np.iinfo(np.int32).max
+    assert run("Max", d, 0, np.float32) == np.finfo(np.float32).min  # lowest(), not min()
+
+
+def test_float_max_all_negative(gpu):
+    # The reference's Max init numeric_limits<float>::min() would return 1.17e-38 here.
+    import gpu_util as g
+
+    a = -np.abs(g.random_array(np.float32, 10_000, 5)) - 1
+    assert run("Max", g.to_dev(a), a.size, np.float32) == a.max()
+
+
+def test_float_sum_deterministic(gpu):
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 24
+    d = datagen.normal_f32(n)
+    r1, r2 = run("Sum", d, n, np.float32), run("Sum", d, n, np.float32)
+    assert np.float32(r1).tobytes() == np.float32(r2).tobytes()
+
+
+@pytest.mark.parametrize("lg", [24, 28])
+def test_full_size_int32_closed_form(gpu, lg):
+    # BASELINE config C1 (2^24) and the north-star size (2^28): uniform [-1000, 1000]
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << lg
+    log(f"reduce int32 full n=2^{lg}")
+    d = datagen.reduce_i32(n)
+    got = run("Sum", d, n, np.int32)
+    h = g.to_host(d)
+    exact = int(h.astype(np.int64).sum())
+    assert int(got) == (exact + (1 << 31)) % (1 << 32) - (1 << 31)
+    assert run("Min", d, n, np.int32) == -1000 and run("Max", d, n, np.int32) == 1000
+    # spot-check the generator against the oracle's host restatement
+    assert (h[:4096] == o.gen("reduce_i32", 4096, datagen.SEED_REDUCE)).all()
+
+
+def test_full_size_float32(gpu):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    d = datagen.normal_f32(n)
+    got = run("Sum", d, n, np.float32)
+    s, ab = o.reduce_f64(g.to_host(d))
+    assert abs(float(got) - s) <= RTOL_SUM * ab

@@ -1,0 +1,96 @@
+"""DeviceScan::ExclusiveSum/InclusiveSum on the GPU through the C ABI:
+integers bit-exact (wraparound) against the oracle, floats within
+|y_i - yhat_i| <= 1e-5 * sum_{j<=i}|x_j| of a float64 scan."""
+import numpy as np
+import pytest
+
+from conftest import log
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+RTOL_SCAN = 1e-5
+INT_DTYPES = [np.int32, np.uint32, np.int64, np.uint64]
+
+
+def run(kind, d_in, n, dtype, tmp=None, pad=0):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceScan
+
+    s = DeviceScan()
+    out = g.empty(n, dtype, pad=pad)
+    if tmp is None:
+        tmp = g.temp(DeviceScan.GetTempStorageBytes(np.dtype(dtype).name, n))
+    getattr(s, kind)(tmp, d_in, out, n)
+    return g.to_host(out)
+
+
+def test_kat_ones_reused_temp(gpu):
+    # device_scan_test.cpp:67-108: ones, N = 2^0..2^23, one temp buffer for both scans
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceScan
+
+    for i in range(24):
+        n = 1 << i
+        log(f"scan ones n={n}")
+        d = g.to_dev(np.ones(n, np.uint32))
+        tmp = g.temp(DeviceScan.GetTempStorageBytes("uint32", n))
+        assert (run("ExclusiveSum", d, n, np.uint32, tmp) == np.arange(n, dtype=np.uint32)).all()
+        assert (run("InclusiveSum", d, n, np.uint32, tmp) == np.arange(1, n + 1, dtype=np.uint32)).all()
+
+
+@pytest.mark.parametrize("dtype", INT_DTYPES)
+@pytest.mark.parametrize("n", [1, 2, 2047, 2048, 4095, 4096, 4097, 100_003, 1 << 20])
+@pytest.mark.parametrize("pad", [0, 1])
+def test_integers_vs_oracle(gpu, dtype, n, pad):
+    import gpu_util as g
+
+    a = g.random_array(dtype, n, seed=n + pad)
+    log(f"scan {np.dtype(dtype).name} n={n} pad={pad}")
+    d = g.to_dev(a, pad=pad)
+    assert (run("ExclusiveSum", d, n, dtype, pad=pad) == o.scan(a, False)).all()
+    assert (run("InclusiveSum", d, n, dtype, pad=pad) == o.scan(a, True)).all()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("n", [1, 4097, 1_000_003])
+def test_floats_vs_float64(gpu, dtype, n):
+    import gpu_util as g
+
+    a = g.random_array(dtype, n, seed=7)
+    d = g.to_dev(a)
+    for kind, incl in (("ExclusiveSum", False), ("InclusiveSum", True)):
+        got = run(kind, d, n, dtype).astype(np.float64)
+        ref, ab = o.scan_f64(a, incl)
+        assert (np.abs(got - ref) <= RTOL_SCAN * ab + 1e-30).all()
+
+
+def test_full_size_u32_exclusive_wraparound(gpu):
+    # BASELINE config C2a: 2^28 uint32 in [0, 255]; the total (~3.4e10) wraps mod 2^32
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    log("scan u32 exclusive full 2^28")
+    d = datagen.u8_u32(n)
+    got = run("ExclusiveSum", d, n, np.uint32)
+    h = g.to_host(d)
+    inc = np.cumsum(h, dtype=np.uint32)
+    assert got[0] == 0 and (got[1:] == inc[:-1]).all()
+    assert int(inc[-1]) == int(h.astype(np.uint64).sum()) % (1 << 32)
+
+
+def test_full_size_f32_inclusive(gpu):
+    # BASELINE config C2b: 2^28 float32 N(0,1), against a float64 scan
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    log("scan f32 inclusive full 2^28")
+    d = datagen.normal_f32(n)
+    got = run("InclusiveSum", d, n, np.float32)
+    h = g.to_host(d).astype(np.float64)
+    ref = np.cumsum(h)
+    ab = np.cumsum(np.abs(h))
+    err = np.abs(got.astype(np.float64) - ref)
+    assert (err <= RTOL_SCAN * ab).all(), float((err / ab).max())

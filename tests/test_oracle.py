@@ -1,0 +1,262 @@
+"""Pins the CPU oracle (oracle/lcpp_oracle.c) before it is trusted as the
+parity checker.  Each oracle function is checked against something it does
+not share code with: the reference tests' known answers (golden fixtures
+regenerated with libstdc++), numpy/Python library routines, closed forms,
+published test vectors, and planted mistakes that must be caught."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import golden
+from oracle import oracle as o
+
+SORT_DTYPES = [np.uint32, np.int32, np.float32, np.uint64, np.int64, np.float64]
+
+
+# ------------------------------------------------------------------ generators
+def test_splitmix64_published_vector():
+    # Vigna's splitmix64.c, state 1234567: first five outputs
+    st = ctypes.c_uint64(1234567)
+    got = [o.lib().lcor_splitmix64_next(ctypes.byref(st)) for _ in range(5)]
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                   4593380528125082431, 16408922859458223821]
+
+
+def test_counter_based_word_equals_sequential_stream():
+    st = ctypes.c_uint64(99)
+    seq = [o.lib().lcor_splitmix64_next(ctypes.byref(st)) for _ in range(100)]
+    assert [o.word(99, i) for i in range(100)] == seq
+
+
+def test_generators_ranges_and_distributions():
+    a = o.gen("reduce_i32", 1 << 20, 0xC1)
+    assert a.min() == -1000 and a.max() == 1000 and abs(a.mean()) < 2
+    b = o.gen("u8_u32", 1 << 20, 0xC2A)
+    assert b.min() == 0 and b.max() == 255
+    c = o.gen("normal_f32", 1 << 20, 0xC2B)
+    assert abs(c.mean()) < 0.01 and abs(c.std() - 1) < 0.01
+    d = o.gen("keys_u32_and3", 1 << 20, 1, 2, 3)
+    assert abs((d >> 24 == 0).mean() - (7 / 8) ** 8) < 0.01  # top digit 0 with p = 0.344
+    e = o.gen("keys_u64_low16", 1 << 16, 4)
+    assert (e >> 16 == 0).all()
+    w = o.words(0xC1, 5)
+    ex = ((w >> 32) * 2001 >> 32).astype(np.int64) - 1000
+    assert (a[:5] == ex).all()
+
+
+def test_segments_generator():
+    b, e = o.segments(0xC5E, 0xC5F, 1 << 20, 1 << 13)
+    L = e.astype(np.int64) - b
+    assert b[0] == 0 and e[-1] == 1 << 20 and (b[1:] == e[:-1]).all() and (L >= 0).all()
+    assert 0.03 < (L == 0).mean() < 0.07 and 110 < L.mean() < 150
+
+
+# ------------------------------------------------------------------ reduce
+def test_reduce_kat_ones():
+    # device_reduce_test.cpp:66-90: Sum of N ones == N, N = 2^k + 1
+    for k in range(0, 16):
+        n = (1 << k) + 1
+        assert o.reduce(o.OP_SUM, np.ones(n, np.uint32)) == n
+
+
+def test_reduce_kat_min_max_shuffled():
+    a = golden("reduce_shuffled_4096_i32.bin", np.int32)
+    exp = golden("reduce_shuffled_4096_expect_min_max_sum_i32.bin", np.int32)
+    assert o.reduce(o.OP_MIN, a) == exp[0] == 0
+    assert o.reduce(o.OP_MAX, a) == exp[1] == 4095
+    assert o.reduce(o.OP_SUM, a) == exp[2]
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint32, np.int64, np.uint64])
+def test_reduce_integer_closed_form(dt):
+    rng = np.random.default_rng(1)
+    info = np.iinfo(dt)
+    a = rng.integers(info.min, info.max, size=100_003, dtype=dt, endpoint=True)
+    bits = 8 * a.itemsize
+    exact = sum(int(x) for x in a) % (1 << bits)  # Python big ints, then wrap
+    got = int(o.reduce(o.OP_SUM, a)) % (1 << bits)
+    assert got == exact
+    assert o.reduce(o.OP_MIN, a) == a.min() and o.reduce(o.OP_MAX, a) == a.max()
+    assert o.reduce(o.OP_SUM, a, nthreads=5) == o.reduce(o.OP_SUM, a)
+
+
+def test_reduce_empty_gives_init():
+    assert o.reduce(o.OP_SUM, np.zeros(0, np.int32)) == 0
+    assert o.reduce(o.OP_MIN, np.zeros(0, np.int32)) == np.iinfo(np.int32).max
+    assert o.reduce(o.OP_MAX, np.zeros(0, np.float32)) == np.finfo(np.float32).min  # lowest()
+
+
+def test_reduce_f64_against_fsum():
+    import math
+
+    a = o.gen("normal_f32", 200_001, 7)
+    s, ab = o.reduce_f64(a)
+    assert s == pytest.approx(math.fsum(float(x) for x in a), abs=1e-9)
+    assert ab == pytest.approx(float(np.abs(a.astype(np.float64)).sum()), rel=1e-12)
+
+
+# ------------------------------------------------------------------ scan
+def test_scan_kat_ones():
+    # device_scan_test.cpp:67-108: ones -> exclusive i, inclusive i+1
+    for k in range(0, 16, 3):
+        n = 1 << k
+        x = np.ones(n, np.uint32)
+        assert (o.scan(x, False) == np.arange(n, dtype=np.uint32)).all()
+        assert (o.scan(x, True) == np.arange(1, n + 1, dtype=np.uint32)).all()
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint32, np.int64, np.uint64])
+def test_scan_wraparound_vs_numpy(dt):
+    rng = np.random.default_rng(2)
+    info = np.iinfo(dt)
+    a = rng.integers(info.min, info.max, size=50_000, dtype=dt, endpoint=True)
+    inc = np.cumsum(a, dtype=dt)  # numpy wraps in the element type
+    exc = np.concatenate([np.zeros(1, dt), inc[:-1]])
+    assert (o.scan(a, True) == inc).all()
+    assert (o.scan(a, False) == exc).all()
+    assert (o.scan(a, True, nthreads=4) == inc).all()
+
+
+@pytest.mark.parametrize("inclusive", [False, True])
+def test_scan_mt_lookback_equals_sequential(inclusive):
+    a = o.gen("u8_u32", 1_000_003, 3)
+    assert (o.scan(a, inclusive, nthreads=6) == o.scan(a, inclusive)).all()
+
+
+def test_scan_f64_against_numpy():
+    a = o.gen("normal_f32", 100_000, 11)
+    ref, ab = o.scan_f64(a, True)
+    np.testing.assert_allclose(ref, np.cumsum(a.astype(np.float64)), rtol=0, atol=1e-9)
+    np.testing.assert_allclose(ab, np.cumsum(np.abs(a.astype(np.float64))), rtol=1e-12)
+    ex, _ = o.scan_f64(a, False)
+    assert ex[0] == 0 and np.allclose(ex[1:], ref[:-1], atol=1e-9)
+
+
+def test_lookback_kat_102400_tiles():
+    # decoupled_look_back.cpp:57-174: aggregate 1 per tile -> exclusive i, inclusive i+1
+    ex, inc = o.lookback_kat(102400, 8)
+    assert (ex == np.arange(102400)).all() and (inc == np.arange(1, 102401)).all()
+
+
+# ------------------------------------------------------------------ radix sort
+@pytest.mark.parametrize("dt", SORT_DTYPES)
+@pytest.mark.parametrize("nthreads", [1, 4])
+def test_sort_keys_vs_numpy(dt, nthreads):
+    rng = np.random.default_rng(3)
+    n = 70_001
+    if np.issubdtype(dt, np.floating):
+        a = (rng.standard_normal(n) * 1e3).astype(dt)
+        a[::97] = 0.0
+        a[::89] = -0.0
+    else:
+        info = np.iinfo(dt)
+        a = rng.integers(info.min, info.max, size=n, dtype=dt, endpoint=True)
+    got = o.radix_sort(a, nthreads=nthreads, tile_items=1024)
+    ref = np.sort(a, kind="stable")
+    assert (got == ref).all()  # value equality (+0 == -0)
+    # stability of +-0: the original order of zeros is kept
+    if np.issubdtype(dt, np.floating):
+        zeros_in = np.signbit(a[a == 0])
+        zeros_out = np.signbit(got[got == 0])
+        assert (zeros_in == zeros_out).all()
+
+
+def test_sort_kat_reversed_keys():
+    # device_radix_sort_one_sweep.cpp:120-151: keys N-1..0
+    for k in (0, 1, 5, 12, 17):
+        n = 1 << k
+        a = np.arange(n - 1, -1, -1, dtype=np.uint32)
+        assert (o.radix_sort(a, tile_items=512) == np.arange(n, dtype=np.uint32)).all()
+
+
+@pytest.mark.parametrize("n", [32, 256, 4096])
+def test_sort_kat_float_golden(n):
+    # device_radix_sort_one_sweep.cpp:61-118 (ascending and descending)
+    asc = golden(f"sort_float_{n}_asc_in_f32.bin", np.float32)
+    desc = golden(f"sort_float_{n}_desc_in_f32.bin", np.float32)
+    assert (o.radix_sort(asc) == golden(f"sort_float_{n}_asc_expect_f32.bin", np.float32)).all()
+    assert (o.radix_sort(desc, descending=True) == golden(f"sort_float_{n}_desc_expect_f32.bin", np.float32)).all()
+
+
+def test_sort_kat_pairs_golden():
+    k = golden("sort_pairs_16384_keys_in_u32.bin", np.uint32)
+    v = golden("sort_pairs_16384_vals_in_f32.bin", np.float32)
+    ko, vo = o.radix_sort(k, v, nthreads=3, tile_items=1024)
+    assert (ko == golden("sort_pairs_16384_keys_expect_u32.bin", np.uint32)).all()
+    assert (vo == golden("sort_pairs_16384_vals_expect_f32.bin", np.float32)).all()
+
+
+def test_sort_pairs_stability_vs_numpy_argsort():
+    k = o.gen("keys_u64_low16", 300_000, 4)
+    v = np.arange(k.size, dtype=np.uint32)
+    ko, vo = o.radix_sort(k, v, nthreads=4, tile_items=2048)
+    perm = np.argsort(k, kind="stable")
+    assert (vo == perm).all() and (ko == k[perm]).all()
+    assert o.check_stable_pairs_u64_u32(k, ko, vo)
+
+
+def test_stability_checker_catches_planted_mistakes():
+    k = o.gen("keys_u64_low16", 50_000, 5) & np.uint64(0xFF)  # many duplicates
+    v = np.arange(k.size, dtype=np.uint32)
+    ko, vo = o.radix_sort(k, v)
+    assert o.check_stable_pairs_u64_u32(k, ko, vo)
+    # swap two equal keys' values -> unstable
+    i = int(np.nonzero(ko[1:] == ko[:-1])[0][0])
+    vo2 = vo.copy(); vo2[[i, i + 1]] = vo2[[i + 1, i]]
+    assert not o.check_stable_pairs_u64_u32(k, ko, vo2)
+    # duplicate a value -> not a permutation
+    vo3 = vo.copy(); vo3[5] = vo3[6]
+    assert not o.check_stable_pairs_u64_u32(k, ko, vo3)
+    # break key order
+    ko4 = ko.copy(); ko4[[0, -1]] = ko4[[-1, 0]]
+    assert not o.check_stable_pairs_u64_u32(k, ko4, vo)
+
+
+def test_sorted_permutation_checker():
+    a = o.gen("keys_u32", 100_000, 6)
+    s = np.sort(a)
+    assert o.check_sorted_permutation_u32(a, s)
+    s2 = s.copy(); s2[100] = s2[101]  # keeps order, changes multiset (if distinct)
+    if s[100] != s[101]:
+        assert not o.check_sorted_permutation_u32(a, s2)
+    s3 = s.copy(); s3[[10, 20]] = s3[[20, 10]]
+    assert not o.check_sorted_permutation_u32(a, s3) or s[10] == s[20]
+
+
+def test_sort_lsd_mistake_is_caught():
+    """A planted mistake in a sort (one 8-bit digit pass skipped) must be
+    visible to the same comparison the GPU parity tests use."""
+    a = o.gen("keys_u32", 10_000, 7)
+    bad = a[np.argsort(a & np.uint32(0xFFFF00FF), kind="stable")]
+    assert not (bad == o.radix_sort(a)).all()
+
+
+# ------------------------------------------------------------------ segment reduce
+def test_segment_reduce_kat_golden():
+    # device_segment_reduce.cpp:62-125
+    a = golden("segment_shuffled_1024_i32.bin", np.int32)
+    b = golden("segment_shuffled_1024_begin_u32.bin", np.uint32)
+    e = golden("segment_shuffled_1024_end_u32.bin", np.uint32)
+    exp = golden("segment_shuffled_1024_expect_i32.bin", np.int32)
+    assert (o.segment_reduce(o.OP_SUM, a, b, e) == exp).all()
+
+
+def test_segment_reduce_vs_numpy():
+    b, e = o.segments(1, 2, 200_000, 1500)
+    a = o.gen("reduce_i32", 200_000, 3)
+    ref = np.array([a[x:y].astype(np.int64).sum() for x, y in zip(b, e)]).astype(np.int32)
+    assert (o.segment_reduce(o.OP_SUM, a, b, e) == ref).all()
+    assert (o.segment_reduce_mt(a, b, e, 4) == ref).all()
+    f = o.gen("normal_f32", 200_000, 3)
+    s, ab = o.segment_reduce_f64(f, b, e)
+    ref64 = np.array([f[x:y].astype(np.float64).sum() for x, y in zip(b, e)])
+    np.testing.assert_allclose(s, ref64, rtol=0, atol=1e-9)
+    assert (s[b == e] == 0).all()
+
+
+def test_segment_reduce_empty_and_inverted_segments():
+    a = np.arange(10, dtype=np.int32)
+    b = np.array([0, 3, 3, 7, 9], np.uint32)
+    e = np.array([3, 3, 1, 10, 9], np.uint32)  # [0,3), empty, inverted (empty), [7,10), empty
+    assert list(o.segment_reduce(o.OP_SUM, a, b, e)) == [3, 0, 0, 24, 0]
