@@ -164,6 +164,50 @@ __device__ __forceinline__ void st16_nt(void *p, u32x4 v)
     __builtin_nontemporal_store(v, static_cast<u32x4 *>(p));
 }
 
+// Split a 16-byte vector into 4 or 2 elements of T and back.  The vector
+// components are copied into scalars first: clang folds
+// __builtin_bit_cast(T, v.y) on an ext_vector component to component 0.
+template <class T>
+__device__ __forceinline__ void unpack16(u32x4 v, T (&out)[16 / sizeof(T)])
+{
+    const uint32_t a = v.x, b = v.y, c = v.z, d = v.w;
+    if constexpr (sizeof(T) == 4) {
+        out[0] = __builtin_bit_cast(T, a);
+        out[1] = __builtin_bit_cast(T, b);
+        out[2] = __builtin_bit_cast(T, c);
+        out[3] = __builtin_bit_cast(T, d);
+    } else {
+        static_assert(sizeof(T) == 8, "4- or 8-byte types only");
+        const uint64_t lo = ((uint64_t)b << 32) | a;
+        const uint64_t hi = ((uint64_t)d << 32) | c;
+        out[0] = __builtin_bit_cast(T, lo);
+        out[1] = __builtin_bit_cast(T, hi);
+    }
+}
+template <class T>
+__device__ __forceinline__ u32x4 pack16(const T (&in)[16 / sizeof(T)])
+{
+    u32x4 v;
+    if constexpr (sizeof(T) == 4) {
+        const uint32_t a = __builtin_bit_cast(uint32_t, in[0]);
+        const uint32_t b = __builtin_bit_cast(uint32_t, in[1]);
+        const uint32_t c = __builtin_bit_cast(uint32_t, in[2]);
+        const uint32_t d = __builtin_bit_cast(uint32_t, in[3]);
+        v.x = a;
+        v.y = b;
+        v.z = c;
+        v.w = d;
+    } else {
+        const uint64_t lo = __builtin_bit_cast(uint64_t, in[0]);
+        const uint64_t hi = __builtin_bit_cast(uint64_t, in[1]);
+        v.x = (uint32_t)lo;
+        v.y = (uint32_t)(lo >> 32);
+        v.z = (uint32_t)hi;
+        v.w = (uint32_t)(hi >> 32);
+    }
+    return v;
+}
+
 // ---------------------------------------------------------------- misc
 // Upper bound on the polls of one look-back wait (~1 s of s_sleep-paced
 // polling).  A wait that exceeds it gives up, so a kernel always drains even

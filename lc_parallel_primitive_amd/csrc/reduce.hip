@@ -49,15 +49,10 @@ RedGrid red_grid(uint64_t n)
 template <class T, class Op>
 __device__ __forceinline__ T fold16(T acc, u32x4 v, Op op)
 {
-    if constexpr (sizeof(T) == 4) {
-        acc = op(acc, __builtin_bit_cast(T, v.x));
-        acc = op(acc, __builtin_bit_cast(T, v.y));
-        acc = op(acc, __builtin_bit_cast(T, v.z));
-        acc = op(acc, __builtin_bit_cast(T, v.w));
-    } else {
-        acc = op(acc, __builtin_bit_cast(T, ((uint64_t)v.y << 32) | v.x));
-        acc = op(acc, __builtin_bit_cast(T, ((uint64_t)v.w << 32) | v.z));
-    }
+    T e[16 / sizeof(T)];
+    unpack16<T>(v, e);
+#pragma unroll
+    for (int j = 0; j < (int)(16 / sizeof(T)); ++j) acc = op(acc, e[j]);
     return acc;
 }
 

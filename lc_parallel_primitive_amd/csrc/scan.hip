@@ -194,16 +194,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ 
     if (full && vec_ok) {
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            const u32x4 v = ld16_nt(in + base + (uint64_t)k * kScanBlock * V + (uint64_t)tid * V);
-            if constexpr (V == 4) {
-                x[k][0] = __builtin_bit_cast(T, v.x);
-                x[k][1] = __builtin_bit_cast(T, v.y);
-                x[k][2] = __builtin_bit_cast(T, v.z);
-                x[k][3] = __builtin_bit_cast(T, v.w);
-            } else {
-                x[k][0] = __builtin_bit_cast(T, ((uint64_t)v.y << 32) | v.x);
-                x[k][1] = __builtin_bit_cast(T, ((uint64_t)v.w << 32) | v.z);
-            }
+            unpack16<T>(ld16_nt(in + base + (uint64_t)k * kScanBlock * V + (uint64_t)tid * V), x[k]);
         }
     } else {
 #pragma unroll
@@ -267,20 +258,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ 
     if (full && vec_ok) {
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            u32x4 v;
-            if constexpr (V == 4) {
-                v.x = __builtin_bit_cast(uint32_t, y[k][0]);
-                v.y = __builtin_bit_cast(uint32_t, y[k][1]);
-                v.z = __builtin_bit_cast(uint32_t, y[k][2]);
-                v.w = __builtin_bit_cast(uint32_t, y[k][3]);
-            } else {
-                const uint64_t a = __builtin_bit_cast(uint64_t, y[k][0]);
-                const uint64_t c = __builtin_bit_cast(uint64_t, y[k][1]);
-                v.x = (uint32_t)a;
-                v.y = (uint32_t)(a >> 32);
-                v.z = (uint32_t)c;
-                v.w = (uint32_t)(c >> 32);
-            }
+            const u32x4 v = pack16<T>(y[k]);
             st16_nt(out + base + (uint64_t)k * kScanBlock * V + (uint64_t)tid * V, v);
         }
     } else {

@@ -71,7 +71,8 @@ def test_empty_gives_init(gpu):
     d = g.empty(4, np.int32)
     assert run("Sum", d, 0, np.int32) == 0
     assert run("Min", d, 0, np.int32) == np.iinfo(np.int32).max
-    assert run("Max", d, 0, np.float32) == np.finfo(np.float32).min  # lowest(), not min()
+    f = g.empty(4, np.float32)
+    assert run("Max", f, 0, np.float32) == np.finfo(np.float32).min  # lowest(), not min()
 
 
 def test_float_max_all_negative(gpu):
