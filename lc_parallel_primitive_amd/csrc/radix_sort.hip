@@ -6,33 +6,47 @@
 // :43-500, block/block_radix_rank.h:66-336, agent/radix_rank_sort_operations.h,
 // common/util_type.h:98-175 (twiddles), common/utils.h:273-324 (MatchAny).
 //
-// MI355X design (all HBM-bound integer/byte work, no MFMA):
-//  * launch 0 "rs_init": zero the P digit histograms and the P tile tickets.
-//  * launch 1 "rs_histogram": one read of the keys builds all P = sizeof(K)
-//    8-bit digit histograms in LDS (one copy per wave to split same-address
-//    atomic traffic), flushed with one global atomic per non-zero bin; the
-//    same kernel zeroes the look-back region of pass 0.
-//  * launches 2..P+1 "rs_onesweep": one tile of 256 x IPT keys per
-//    workgroup, tile index from a dynamic ticket.  Keys are loaded
-//    wave-striped (lane l of wave w, item u -> key w*64*IPT + u*64 + l), so
-//    processing items in order u and lanes in order l visits keys in input
-//    order.  Ranking: the 64-lane peer mask of equal digits comes from 8
-//    ballots (wave64 MatchAny); each lane's rank inside its wave and digit is
-//    counter + popcount(peers below it), and the lowest peer advances the
-//    wave's LDS counter.  No LDS atomics, ranks are stable.  Thread d then
-//    owns digit d: it sums the wave counters, publishes the tile count
-//    (PARTIAL) at once, takes the tile's exclusive digit prefix with a
-//    workgroup scan and walks back over earlier tiles until a GLOBAL word
-//    (the tile-0 word carries the pass's global digit base, so every GLOBAL
-//    word is already an absolute output offset).  Keys are scattered into
-//    LDS in sorted order and written out so that consecutive threads write
-//    consecutive positions of each digit run.  Values follow with the same
-//    ranks.
-//  * Look-back words are 32-bit {GLOBAL:1 | PARTIAL:1 | count:30}, polled
-//    with agent-scope atomic loads (the 8 XCD L2s are not coherent).  Two
+// MI355X design (HBM-bound integer/byte work, no MFMA).  Measured on the
+// device: a cross-workgroup publish is observed ~0.5 us later, and 65536
+// same-address atomics take ~0.75 ms.  The reference's shape (1024-key tiles,
+// a per-tile ticket, a per-digit walk over every earlier tile) therefore
+// cannot keep up at 8 TB/s: at the tile rate the pass needs, each tile would
+// walk ~100 predecessors per digit.  The pass here is built around that:
+//
+//  * launch 0 "rs_init": zero the P digit histograms.
+//  * launch 1 "rs_histogram": one 1024-thread workgroup per CU streams a
+//    contiguous chunk of keys and counts all P = sizeof(K) 8-bit digits at
+//    once into an LDS table with 32 (16 for 8-byte keys) lane-private copies
+//    of every counter, so that equal digits in one wave (skewed or constant
+//    key bytes) never hit one LDS address; flushed with one global atomic per
+//    non-zero bin.  It also zeroes the look-back state of pass 0.
+//  * launches 2..P+1 "rs_onesweep": one 16384-key tile (8192 for 8-byte keys
+//    or values) per 512-thread workgroup, keys staged in LDS.  No ticket:
+//    tiles are mapped from the workgroup id so that every 8 consecutive
+//    tiles run on one XCD (workgroups are dispatched round-robin over the 8
+//    XCDs), which lets that XCD's L2 merge the adjacent digit runs the 8
+//    tiles write; a tile only ever waits on tiles dispatched at most 63
+//    workgroups after it.  Ranking: keys are loaded wave-striped (lane l of
+//    wave w, item u -> key w*64*IPT + u*64 + l) so items in order u and lanes
+//    in order l are input order; a key's rank in its (wave, digit) is one
+//    returning LDS atomic add on the wave's counter for that digit.  gfx950
+//    serves same-address LDS atomics of one instruction in lane order, so
+//    the ranks are stable (an in-bounds probe found no exception in 5e8
+//    lane-operations over uniform, skewed and constant digits; the parity
+//    tests check stability on every run).
+//  * Two-level decoupled look-back.  Tiles form batches of 8.  Each tile
+//    publishes its 256 digit counts once.  A tile's exclusive prefix = the
+//    exclusive prefix of its batch + the counts of the earlier tiles of its
+//    batch (at most 7 parallel reads per digit).  The last tile of a batch
+//    publishes the batch aggregate (PARTIAL) as soon as it has its
+//    batch-mates' counts and the batch's inclusive prefix (GLOBAL) after a
+//    windowed walk over earlier batch words.  Every wait is on an earlier
+//    tile.  Words are 32-bit {GLOBAL:1 | PARTIAL:1 | value:30}, accessed
+//    with agent-scope atomics (the 8 XCD L2s are not coherent).  Two look-back
 //    regions alternate between passes and each tile clears its own slots of
-//    the other region for the next pass, so there is no per-pass memset
-//    launch (the reference resets 256 MiB per pass, device_radix_sort.h:341).
+//    the other region for the next pass (no per-pass memset launch).
+//  * Keys leave LDS in sorted order: consecutive threads write consecutive
+//    positions of each digit run.  Values follow with the same ranks.
 //  * Keys-only sorts reserve no value scratch (the reference reserves N
 //    values it never uses, device_radix_sort.h:118-122).
 #include "common.hpp"
@@ -40,10 +54,13 @@
 namespace lcpp {
 namespace {
 
-constexpr int kRsBlock = 256;
-constexpr int kRsWaves = kRsBlock / kWave;
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 256;
+constexpr int kOsBlock = 512;  // onesweep workgroup
+constexpr int kOsWaves = kOsBlock / kWave;
+constexpr int kBatch = 8;      // tiles per look-back batch
+constexpr int kBatchWindow = 4;
+constexpr int kHistBlock = 1024;
 constexpr uint32_t kLbGlobal = 0x80000000u;
 constexpr uint32_t kLbPartial = 0x40000000u;
 constexpr uint32_t kLbMask = 0x3FFFFFFFu;
@@ -81,54 +98,63 @@ __device__ __forceinline__ uint32_t digit_of(UK tk, uint32_t shift)
     return (uint32_t)(tk >> shift) & (kRadix - 1);
 }
 
-// 64-lane mask of the lanes whose 8-bit digit equals this lane's.
-__device__ __forceinline__ uint64_t match_digit(uint32_t d)
-{
-    uint64_t m = ~0ull;
-#pragma unroll
-    for (int b = 0; b < kRadixBits; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t bal = ballot(bit);
-        m &= bit ? bal : ~bal;
-    }
-    return m;
-}
-
-// Exclusive scan of one value per thread over the 256-thread workgroup.
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t x, uint32_t *s_wsum)
+// Exclusive scan of the values x held by threads 0..255 (one digit each) of
+// the workgroup; other threads pass 0 and get garbage.  Every thread of the
+// workgroup must call it (it contains a barrier).
+__device__ __forceinline__ uint32_t digit_excl_scan(uint32_t x, uint32_t *s_wsum)
 {
     const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
     const uint32_t inc = wave_inclusive_scan(x, SumOp());
-    if (lane == kWave - 1) s_wsum[wave] = inc;
+    if (lane == kWave - 1 && wave < kRadix / kWave) s_wsum[wave] = inc;
     __syncthreads();
     uint32_t pre = 0;
 #pragma unroll
-    for (int w = 0; w < kRsWaves; ++w)
+    for (int w = 0; w < kRadix / kWave; ++w)
         if ((uint32_t)w < wave) pre += s_wsum[w];
     return pre + inc - x;
 }
 
+// Poll a look-back word until it is published (bounded: a wait that never
+// ends would mean a broken invariant; it then gives up with value 0).
+__device__ __forceinline__ uint32_t wait_word(const uint32_t *p, uint32_t w)
+{
+    for (uint32_t spins = 0; w == 0 && spins < kSpinLimit; ++spins) {
+        __builtin_amdgcn_s_sleep(1);
+        w = ld_relaxed(p);
+    }
+    return w ? w : kLbGlobal;
+}
+
 // ------------------------------------------------------------------ init
-__global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *bins, uint32_t nbins,
-                                                      uint32_t *tickets, uint32_t ntickets)
+__global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *bins, uint32_t nbins)
 {
     for (uint32_t i = threadIdx.x; i < nbins; i += 256) bins[i] = 0;
-    for (uint32_t i = threadIdx.x; i < ntickets; i += 256) tickets[i] = 0;
 }
 
 // ------------------------------------------------------------------ histogram
+template <class UK>
+constexpr int hist_copies()
+{
+    return sizeof(UK) == 4 ? 32 : 16;  // 128 KB of LDS either way
+}
+template <class UK>
+constexpr size_t hist_lds_bytes()
+{
+    return sizeof(UK) * kRadix * hist_copies<UK>() * 4;
+}
+
 template <class UK, int KIND>
-__global__ __launch_bounds__(kRsBlock) void rs_histogram_kernel(const UK *__restrict__ keys,
-                                                                uint64_t n, uint64_t chunk,
-                                                                uint32_t *__restrict__ bins,
-                                                                uint32_t *__restrict__ lb0,
-                                                                uint64_t lb0_words)
+__global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
+    const UK *__restrict__ keys, uint64_t n, uint64_t chunk, uint32_t *__restrict__ bins,
+    uint32_t *__restrict__ clear0, uint64_t clear0_words, uint32_t *__restrict__ clear1,
+    uint64_t clear1_words)
 {
     constexpr int P = sizeof(UK);
-    __shared__ uint32_t s_hist[kRsWaves][P][kRadix];
+    constexpr int C = hist_copies<UK>();
+    extern __shared__ uint32_t s_hist[];  // [P][256][C]
     const uint32_t tid = threadIdx.x;
-    const uint32_t wave = tid / kWave;
-    for (uint32_t i = tid; i < kRsWaves * P * kRadix; i += kRsBlock) (&s_hist[0][0][0])[i] = 0;
+    const uint32_t copy = lane_id() % C;
+    for (uint32_t i = tid; i < (uint32_t)(P * kRadix * C); i += kHistBlock) s_hist[i] = 0;
     __syncthreads();
 
     const uint64_t b0 = (uint64_t)blockIdx.x * chunk;
@@ -136,81 +162,94 @@ __global__ __launch_bounds__(kRsBlock) void rs_histogram_kernel(const UK *__rest
     auto count = [&](UK raw) {
         const UK tk = tw_in<UK, KIND>(raw);
 #pragma unroll
-        for (int p = 0; p < P; ++p) atomicAdd(&s_hist[wave][p][digit_of<UK, KIND>(tk, p * kRadixBits)], 1u);
+        for (int p = 0; p < P; ++p)
+            atomicAdd(&s_hist[((uint32_t)p * kRadix + digit_of<UK, KIND>(tk, p * kRadixBits)) * C + copy], 1u);
     };
     constexpr uint64_t V = 16 / sizeof(UK);
-    constexpr uint64_t step = (uint64_t)kRsBlock * V * 4;
+    constexpr int kVecs = 4;
+    constexpr uint64_t step = (uint64_t)kHistBlock * V * kVecs;
     uint64_t tail = b0;
     if ((reinterpret_cast<uintptr_t>(keys) & 15) == 0) {
         const uint64_t full_end = b0 + (b1 - b0) / step * step;
         for (uint64_t t = b0; t < full_end; t += step) {
-            u32x4 v[4];
+            u32x4 v[kVecs];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                v[i] = ld16_nt((keys + t + ((uint64_t)i * kRsBlock + tid) * V));
+            for (int i = 0; i < kVecs; ++i) v[i] = ld16_nt(keys + t + ((uint64_t)i * kHistBlock + tid) * V);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (sizeof(UK) == 4) {
-                    count(v[i].x);
-                    count(v[i].y);
-                    count(v[i].z);
-                    count(v[i].w);
-                } else {
-                    count(((uint64_t)v[i].y << 32) | v[i].x);
-                    count(((uint64_t)v[i].w << 32) | v[i].z);
-                }
+            for (int i = 0; i < kVecs; ++i) {
+                UK e[V];
+                unpack16<UK>(v[i], e);
+#pragma unroll
+                for (int j = 0; j < (int)V; ++j) count(e[j]);
             }
         }
         tail = full_end;
     }
-    for (uint64_t i = tail + tid; i < b1; i += kRsBlock) count(keys[i]);
+    for (uint64_t i = tail + tid; i < b1; i += kHistBlock) count(keys[i]);
     __syncthreads();
-    for (uint32_t i = tid; i < P * kRadix; i += kRsBlock) {
+    for (uint32_t i = tid; i < (uint32_t)(P * kRadix); i += kHistBlock) {
         uint32_t c = 0;
-#pragma unroll
-        for (int w = 0; w < kRsWaves; ++w) c += (&s_hist[w][0][0])[i];
+#pragma unroll 8
+        for (int k = 0; k < C; ++k) c += s_hist[i * C + k];
         if (c) atomicAdd(&bins[i], c);
     }
-    // zero the pass-0 look-back region
-    const uint64_t stride = (uint64_t)gridDim.x * kRsBlock;
-    for (uint64_t i = (uint64_t)blockIdx.x * kRsBlock + tid; i < lb0_words; i += stride) lb0[i] = 0;
+    // zero the look-back state of pass 0
+    const uint64_t stride = (uint64_t)gridDim.x * kHistBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear0_words; i += stride) clear0[i] = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear1_words; i += stride) clear1[i] = 0;
 }
 
 // ------------------------------------------------------------------ onesweep pass
 template <int IPT, class UK, class UV>
 struct OnesweepSmem {
-    static constexpr int TILE = kRsBlock * IPT;
+    static constexpr int TILE = kOsBlock * IPT;
     union {
         UK keys[TILE];
         UV vals[TILE];
     };
-    uint32_t cnt[kRsWaves][kRadix];  // per-wave digit counters, then wave prefixes
-    uint32_t dexcl[kRadix];          // tile exclusive digit prefix
-    uint32_t goff[kRadix];           // output offset of sorted tile position 0 of digit d
-    uint32_t wsum[2][kRsWaves];
-    uint32_t tile;
+    uint32_t cnt[kOsWaves][kRadix];  // per-wave digit counters, then wave prefixes
+    uint32_t goff[kRadix];           // output position of sorted tile position 0 of digit d
+    uint32_t wsum[2][kRadix / kWave];
 };
 
-template <int IPT, class UK, class UV, int KIND, bool PAIRS>
-__global__ __launch_bounds__(kRsBlock) void rs_onesweep_kernel(
-    const UK *__restrict__ kin, UK *__restrict__ kout, const UV *__restrict__ vin,
-    UV *__restrict__ vout, uint32_t n, uint32_t shift, uint32_t *__restrict__ tickets,
-    const uint32_t *__restrict__ bins, uint32_t *__restrict__ lb, uint32_t *__restrict__ lb_next)
+// Look-back state of one pass: tcount[tiles][256] (tile digit counts,
+// written once) and bword[batches][256] (batch aggregate, then batch
+// inclusive prefix).
+struct LbState {
+    uint32_t *tcount, *bword;            // this pass
+    uint32_t *tcount_next, *bword_next;  // the other region, cleared for the next pass
+};
+
+// Workgroup -> tile: in every full group of 64 workgroups, b = 64q + 8j + x
+// (x = the XCD that b is dispatched to) processes tile 64q + 8x + j, so the 8
+// tiles 64q + 8x .. +7 run on XCD x.  A partial last group maps identically.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t grid)
 {
-    constexpr int TILE = kRsBlock * IPT;
+    constexpr uint32_t kGroup = 64;
+    const uint32_t g = b / kGroup;
+    if ((g + 1) * kGroup > grid) return b;
+    const uint32_t r = b % kGroup;
+    return g * kGroup + (r % 8) * 8 + r / 8;
+}
+
+template <int IPT, class UK, class UV, int KIND, bool PAIRS>
+__global__ __launch_bounds__(kOsBlock) void rs_onesweep_kernel(
+    const UK *__restrict__ kin, UK *__restrict__ kout, const UV *__restrict__ vin,
+    UV *__restrict__ vout, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
+    LbState lb)
+{
+    constexpr int TILE = kOsBlock * IPT;
     constexpr int WAVE_ITEMS = kWave * IPT;
     __shared__ OnesweepSmem<IPT, UK, UV> sm;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
-
-    for (int w = 0; w < kRsWaves; ++w) sm.cnt[w][tid] = 0;
-    if (tid == 0) sm.tile = ticket(tickets);
-    __syncthreads();
-    const uint32_t tile = sm.tile;
-    const uint32_t base = tile * TILE;
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t base = tile * (uint32_t)TILE;
     const uint32_t valid = n - base < (uint32_t)TILE ? n - base : (uint32_t)TILE;
+
+    for (uint32_t i = tid; i < (uint32_t)(kOsWaves * kRadix); i += kOsBlock) (&sm.cnt[0][0])[i] = 0;
 
     // ---- load (wave-striped), twiddle; pads are all-ones -> digit 255, last
     UK tk[IPT];
@@ -231,78 +270,110 @@ __global__ __launch_bounds__(kRsBlock) void rs_onesweep_kernel(
             if constexpr (PAIRS) v[u] = idx < n ? vin[idx] : UV(0);
         }
     }
+    __syncthreads();  // counters zeroed
 
-    // ---- stable rank within (wave, digit)
+    // ---- stable rank within (wave, digit): lane-ordered LDS atomics
     uint32_t rank[IPT];
     uint32_t *cnt = sm.cnt[wave];
 #pragma unroll
-    for (int u = 0; u < IPT; ++u) {
-        const uint32_t d = digit_of<UK, KIND>(tk[u], shift);
-        const uint64_t peers = match_digit(d);
-        const uint32_t below = mask_rank(peers);
-        const uint32_t c = cnt[d];
-        rank[u] = c + below;
-        if (below == 0) cnt[d] = c + (uint32_t)__popcll(peers);
-    }
+    for (int u = 0; u < IPT; ++u) rank[u] = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u], shift)], 1u);
     __syncthreads();
 
-    // ---- thread d owns digit d
-    const uint32_t d = tid;
+    // ---- threads 0..255 own digit d: tile counts, publish, clear next slots
+    const bool owner = tid < (uint32_t)kRadix;
+    const uint32_t d = owner ? tid : 0u;
+    const uint32_t batch = tile / kBatch;
+    const uint32_t bpos = tile % kBatch;
+    const bool batch_last = bpos == kBatch - 1;
     uint32_t total = 0;
+    if (owner) {
 #pragma unroll
-    for (int w = 0; w < kRsWaves; ++w) {
-        const uint32_t c = sm.cnt[w][d];
-        sm.cnt[w][d] = total;  // wave prefix within the tile
-        total += c;
+        for (int w = 0; w < kOsWaves; ++w) {
+            const uint32_t c = sm.cnt[w][d];
+            sm.cnt[w][d] = total;  // wave prefix within the tile
+            total += c;
+        }
+        if (d == kRadix - 1) total -= (uint32_t)TILE - valid;  // drop the pads
+        st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], total | kLbPartial);
+        lb.tcount_next[(size_t)tile * kRadix + d] = 0;
+        if (batch_last) lb.bword_next[(size_t)batch * kRadix + d] = 0;
     }
-    if (d == kRadix - 1) total -= (uint32_t)TILE - valid;  // drop the pads
-    if (tile > 0) st_relaxed(&lb[(size_t)tile * kRadix + d], total | kLbPartial);
-    lb_next[(size_t)tile * kRadix + d] = 0;  // slot of the next pass
-    const uint32_t dexcl = block_excl_scan(total, sm.wsum[0]);
-    sm.dexcl[d] = dexcl;
+    const uint32_t dexcl = digit_excl_scan(owner ? total : 0u, sm.wsum[0]);
+    if (owner) {
+#pragma unroll
+        for (int w = 0; w < kOsWaves; ++w) sm.cnt[w][d] += dexcl;  // wave base in the sorted tile
+    }
     uint32_t gbase = 0;
-    if (tile == 0) gbase = block_excl_scan(bins[d], sm.wsum[1]);
+    if (batch == 0) gbase = digit_excl_scan(owner ? bins[d] : 0u, sm.wsum[1]);
+
+    // ---- issue the within-batch count reads before the LDS scatter
+    uint32_t wb[kBatch - 1], bw0[kBatchWindow];
+#pragma unroll
+    for (int k = 0; k < kBatch - 1; ++k)
+        wb[k] = owner && (uint32_t)k < bpos ? ld_relaxed(&lb.tcount[(size_t)(tile - bpos + k) * kRadix + d]) : 0u;
+#pragma unroll
+    for (int k = 0; k < kBatchWindow; ++k)
+        bw0[k] = owner && (int64_t)batch - 1 - k >= 0 ? ld_relaxed(&lb.bword[(size_t)(batch - 1 - k) * kRadix + d])
+                                                      : kLbGlobal;
     __syncthreads();
 
     // ---- scatter keys into LDS in sorted-tile order
 #pragma unroll
     for (int u = 0; u < IPT; ++u) {
         const uint32_t dd = digit_of<UK, KIND>(tk[u], shift);
-        rank[u] += sm.dexcl[dd] + sm.cnt[wave][dd];
+        rank[u] += sm.cnt[wave][dd];
         sm.keys[rank[u]] = tk[u];
     }
 
-    // ---- decoupled look-back for digit d
-    uint32_t excl;
-    if (tile == 0) {
-        excl = gbase;
-        st_relaxed(&lb[d], (gbase + total) | kLbGlobal);
-    } else {
-        uint32_t acc = 0;
-        int64_t j = (int64_t)tile - 1;
-        for (;;) {
-            const uint32_t *p = &lb[(size_t)j * kRadix + d];
-            uint32_t w = ld_relaxed(p);
-            for (uint32_t spins = 0; w == 0 && spins < kSpinLimit; ++spins) {
-                __builtin_amdgcn_s_sleep(1);
-                w = ld_relaxed(p);
+    // ---- two-level look-back for digit d
+    if (owner) {
+        uint32_t within = 0;
+#pragma unroll
+        for (int k = 0; k < kBatch - 1; ++k) {
+            if ((uint32_t)k < bpos) {
+                const uint32_t w = wait_word(&lb.tcount[(size_t)(tile - bpos + k) * kRadix + d], wb[k]);
+                within += w & kLbMask;
             }
-            if (w == 0) w = kLbGlobal;  // gave up: terminate the walk
-            acc += w & kLbMask;
-            if (w & kLbGlobal) break;
-            --j;
         }
-        excl = acc;
-        st_relaxed(&lb[(size_t)tile * kRadix + d], (acc + total) | kLbGlobal);
+        if (batch_last && batch > 0)
+            st_relaxed(&lb.bword[(size_t)batch * kRadix + d], (within + total) | kLbPartial);
+        uint32_t bexcl;
+        if (batch == 0) {
+            bexcl = gbase;
+        } else {
+            uint32_t acc = 0;
+            int64_t j = (int64_t)batch - 1;
+            bool done = false;
+            bool first = true;
+            while (!done) {
+                uint32_t w[kBatchWindow];
+#pragma unroll
+                for (int k = 0; k < kBatchWindow; ++k)
+                    w[k] = first ? bw0[k] : j - k >= 0 ? ld_relaxed(&lb.bword[(size_t)(j - k) * kRadix + d]) : kLbGlobal;
+                first = false;
+#pragma unroll
+                for (int k = 0; k < kBatchWindow; ++k) {
+                    if (!done) {
+                        const uint32_t wk =
+                            j - k >= 0 ? wait_word(&lb.bword[(size_t)(j - k) * kRadix + d], w[k]) : w[k];
+                        acc += wk & kLbMask;
+                        done = (wk & kLbGlobal) != 0;
+                    }
+                }
+                j -= kBatchWindow;
+            }
+            bexcl = acc;
+        }
+        if (batch_last) st_relaxed(&lb.bword[(size_t)batch * kRadix + d], (bexcl + within + total) | kLbGlobal);
+        sm.goff[d] = bexcl + within - dexcl;
     }
-    sm.goff[d] = excl - dexcl;
     __syncthreads();
 
     // ---- write out: consecutive threads -> consecutive positions of a digit run
     uint32_t dg[PAIRS ? IPT : 1];
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
-        const uint32_t i = j * kRsBlock + tid;
+        const uint32_t i = j * kOsBlock + tid;
         const UK k = sm.keys[i];
         const uint32_t dd = digit_of<UK, KIND>(k, shift);
         if constexpr (PAIRS) dg[j] = dd;
@@ -316,7 +387,7 @@ __global__ __launch_bounds__(kRsBlock) void rs_onesweep_kernel(
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            const uint32_t i = j * kRsBlock + tid;
+            const uint32_t i = j * kOsBlock + tid;
             const uint32_t pos = i + sm.goff[dg[j]];
             if (i < valid && pos < n) vout[pos] = sm.vals[i];
         }
@@ -324,37 +395,52 @@ __global__ __launch_bounds__(kRsBlock) void rs_onesweep_kernel(
 }
 
 // ------------------------------------------------------------------ host side
-template <class UK>
-constexpr int rs_ipt()
-{
-    return sizeof(UK) == 4 ? 16 : 16;
-}
+// Items per thread: 32 (16384-key tiles) when keys and values are 4 bytes,
+// 16 (8192-key tiles) when either is 8 bytes, so the LDS tile stays 64 KB
+// and two workgroups fit a CU.
+constexpr int os_ipt(int key_bytes, int val_bytes) { return key_bytes == 8 || val_bytes == 8 ? 16 : 32; }
 
 struct RsLayout {
-    uint64_t passes, tiles, bins_off, tickets_off, lb_off, lb_words, ktmp_off, vtmp_off, total;
+    uint64_t passes, tiles, batches, bins_off, tc_off, tc_words, bw_off, bw_words, ktmp_off, vtmp_off, total;
 };
 
-RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes, int ipt)
+RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
 {
     RsLayout L{};
     L.passes = (uint64_t)key_bytes;  // 8-bit digits
-    const uint64_t tile = (uint64_t)kRsBlock * ipt;
+    const uint64_t tile = (uint64_t)kOsBlock * os_ipt(key_bytes, val_bytes);
     L.tiles = n ? ceil_div(n, tile) : 0;
+    L.batches = ceil_div(L.tiles, kBatch);
     L.bins_off = 0;
-    L.tickets_off = align_up(L.passes * kRadix * 4, 256);
-    L.lb_off = L.tickets_off + 256;
-    L.lb_words = L.tiles * kRadix;
-    L.ktmp_off = L.lb_off + align_up(2 * L.lb_words * 4, 256);
+    L.tc_off = align_up(L.passes * kRadix * 4, 256);
+    L.tc_words = L.tiles * kRadix;
+    L.bw_off = L.tc_off + align_up(2 * L.tc_words * 4, 256);
+    L.bw_words = L.batches * kRadix;
+    L.ktmp_off = L.bw_off + align_up(2 * L.bw_words * 4, 256);
     L.vtmp_off = L.ktmp_off + align_up(n * key_bytes, 256);
     L.total = L.vtmp_off + align_up(n * val_bytes, 256);
     return L;
+}
+
+int num_cus()
+{
+    static int cached = 0;
+    if (!cached) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            cached = cus;
+        else
+            cached = 256;
+    }
+    return cached;
 }
 
 template <class UK, class UV, int KIND, bool PAIRS>
 int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const void *vin_,
            void *vout_, uint64_t n, hipStream_t s)
 {
-    constexpr int IPT = rs_ipt<UK>();
+    constexpr int IPT = os_ipt(sizeof(UK), PAIRS ? sizeof(UV) : 0);
     if (n == 0) return LCPP_OK;
     if (n > kMaxItems) return LCPP_ERR_INVALID_ARG;
     const UK *kin = static_cast<const UK *>(kin_);
@@ -362,29 +448,40 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     const UV *vin = static_cast<const UV *>(vin_);
     UV *vout = static_cast<UV *>(vout_);
     if (!kin || !kout || (PAIRS && (!vin || !vout))) return LCPP_ERR_INVALID_ARG;
-    const RsLayout L = rs_layout(n, sizeof(UK), PAIRS ? sizeof(UV) : 0, IPT);
+    const RsLayout L = rs_layout(n, sizeof(UK), PAIRS ? sizeof(UV) : 0);
     if (temp_bytes < L.total) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
     char *t = static_cast<char *>(temp);
     uint32_t *bins = reinterpret_cast<uint32_t *>(t + L.bins_off);
-    uint32_t *tickets = reinterpret_cast<uint32_t *>(t + L.tickets_off);
-    uint32_t *lb[2] = {reinterpret_cast<uint32_t *>(t + L.lb_off),
-                       reinterpret_cast<uint32_t *>(t + L.lb_off) + L.lb_words};
+    uint32_t *tc[2] = {reinterpret_cast<uint32_t *>(t + L.tc_off),
+                       reinterpret_cast<uint32_t *>(t + L.tc_off) + L.tc_words};
+    uint32_t *bw[2] = {reinterpret_cast<uint32_t *>(t + L.bw_off),
+                       reinterpret_cast<uint32_t *>(t + L.bw_off) + L.bw_words};
     UK *ktmp = reinterpret_cast<UK *>(t + L.ktmp_off);
     UV *vtmp = reinterpret_cast<UV *>(t + L.vtmp_off);
     const int P = (int)L.passes;
 
-    LCPP_LAUNCH("rs_init", s, rs_init_kernel<<<1, 256, 0, s>>>(bins, P * kRadix, tickets, P));
+    LCPP_LAUNCH("rs_init", s, rs_init_kernel<<<1, 256, 0, s>>>(bins, P * kRadix));
     LCPP_CHECK_LAUNCH();
     {
-        const uint64_t htile = (uint64_t)kRsBlock * 4 * (16 / sizeof(UK));
+        // one 1024-thread workgroup per CU (128 KB of LDS each)
+        static bool lds_set = false;
+        constexpr size_t lds = hist_lds_bytes<UK>();
+        if (!lds_set) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void *>(&rs_histogram_kernel<UK, KIND>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+                return LCPP_ERR_HIP;
+            lds_set = true;
+        }
+        const uint64_t htile = (uint64_t)kHistBlock * 4 * (16 / sizeof(UK));
         const uint64_t htiles = ceil_div(n, htile);
-        uint64_t grid = htiles < 1024 ? htiles : 1024;
+        const uint64_t cus = (uint64_t)num_cus();
+        uint64_t grid = htiles < cus ? htiles : cus;
         const uint64_t chunk = ceil_div(htiles, grid) * htile;
         grid = ceil_div(n, chunk);
         LCPP_LAUNCH("rs_histogram", s,
-                    rs_histogram_kernel<UK, KIND><<<(uint32_t)grid, kRsBlock, 0, s>>>(kin, n, chunk, bins,
-                                                                                      lb[0], L.lb_words));
+                    rs_histogram_kernel<UK, KIND><<<(uint32_t)grid, kHistBlock, lds, s>>>(
+                        kin, n, chunk, bins, tc[0], L.tc_words, bw[0], L.bw_words));
         LCPP_CHECK_LAUNCH();
     }
     // ping-pong so that the last pass lands in the output and the input is preserved
@@ -394,10 +491,11 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         const bool to_out = ((P - 1 - p) % 2) == 0;
         UK *dst_k = to_out ? kout : ktmp;
         UV *dst_v = to_out ? vout : vtmp;
+        const LbState lb{tc[p & 1], bw[p & 1], tc[(p + 1) & 1], bw[(p + 1) & 1]};
         LCPP_LAUNCH("rs_onesweep", s,
-                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS><<<(uint32_t)L.tiles, kRsBlock, 0, s>>>(
+                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
                         src_k, dst_k, src_v, dst_v, (uint32_t)n, (uint32_t)(p * kRadixBits),
-                        tickets + p, bins + p * kRadix, lb[p & 1], lb[(p + 1) & 1])));
+                        bins + p * kRadix, lb)));
         LCPP_CHECK_LAUNCH();
         src_k = dst_k;
         src_v = dst_v;
@@ -445,7 +543,7 @@ extern "C" int lcpp_radix_sort_keys_temp_bytes(lcpp_dtype k, uint64_t n, size_t 
     if (!bytes) return LCPP_ERR_INVALID_ARG;
     const int kb = dtype_bytes(k);
     if (!kb) return LCPP_ERR_UNSUPPORTED_DTYPE;
-    *bytes = rs_layout(n, kb, 0, kb == 4 ? rs_ipt<uint32_t>() : rs_ipt<uint64_t>()).total;
+    *bytes = rs_layout(n, kb, 0).total;
     return LCPP_OK;
 }
 
@@ -455,7 +553,7 @@ extern "C" int lcpp_radix_sort_pairs_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint
     if (!bytes) return LCPP_ERR_INVALID_ARG;
     const int kb = dtype_bytes(k), vb = dtype_bytes(v);
     if (!kb || !vb) return LCPP_ERR_UNSUPPORTED_DTYPE;
-    *bytes = rs_layout(n, kb, vb, kb == 4 ? rs_ipt<uint32_t>() : rs_ipt<uint64_t>()).total;
+    *bytes = rs_layout(n, kb, vb).total;
     return LCPP_OK;
 }
 

@@ -67,10 +67,11 @@ def test_temp_bytes_queries(L):
     # scan: ticket + one packed 64-bit word per 4096-element tile
     rc, b = _q(L.lcpp_scan_temp_bytes, 1, 1 << 28)
     assert rc == 0 and b == 256 + (1 << 16) * 8
-    # sort: bins + tickets + 2 look-back regions + key scratch (no value scratch)
+    # sort: bins + 2 regions of tile counts + 2 regions of batch words + key
+    # scratch (no value scratch for keys-only); 16384-key tiles, batches of 8
     rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, 1 << 28)
-    tiles = (1 << 28) // 4096
-    assert rc == 0 and b == 4 * 256 * 4 + 256 + 2 * tiles * 256 * 4 + (1 << 28) * 4
+    tiles = (1 << 28) // 16384
+    assert rc == 0 and b == 4 * 256 * 4 + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 4 + (1 << 28) * 4
     rc, bp = _q(L.lcpp_radix_sort_pairs_temp_bytes, 4, 1, 1 << 27)
     assert rc == 0 and bp > (1 << 27) * 12
     # segment reduce needs none (as the reference)
