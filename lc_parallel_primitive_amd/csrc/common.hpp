@@ -208,6 +208,57 @@ __device__ __forceinline__ u32x4 pack16(const T (&in)[16 / sizeof(T)])
     return v;
 }
 
+// ---------------------------------------------------------------- raw buffers
+// A raw buffer resource (stride 0) over [p, p + bytes): loads past `bytes`
+// return 0 and stores past it are dropped by the address unit, so a ragged
+// last tile needs no per-element guards.  Word 3 = 0x00020000 selects 32-bit
+// data format, the gfx9-family raw-buffer encoding.  Offsets are 32-bit, so
+// one resource covers < 2 GiB.
+constexpr int kRawBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer builtins on gfx94x/gfx950: bit 1 = nt
+// (streaming, no reuse expected).
+constexpr int kPolicyNT = 2;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, kRawBufferWord3);
+}
+__device__ __forceinline__ u32x4 buf_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kPolicyNT);
+}
+__device__ __forceinline__ void buf_st16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, u32x4 v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, (int)soff, kPolicyNT);
+}
+// One 4- or 8-byte element (0 when out of range).
+template <class T>
+__device__ __forceinline__ T buf_ld_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+    } else {
+        static_assert(sizeof(T) == 8, "4- or 8-byte types only");
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+        const uint32_t lo = w[0], hi = w[1];
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
+template <class T>
+__device__ __forceinline__ void buf_st_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, T v)
+{
+    if constexpr (sizeof(T) == 4) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff, (int)soff, 0);
+    } else {
+        typedef uint32_t u32x2v __attribute__((vector_size(8)));
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        u32x2v w;
+        w[0] = (uint32_t)b;
+        w[1] = (uint32_t)(b >> 32);
+        __builtin_amdgcn_raw_buffer_store_b64(w, r, (int)voff, (int)soff, 0);
+    }
+}
+
 // ---------------------------------------------------------------- misc
 // Upper bound on the polls of one look-back wait (~1 s of s_sleep-paced
 // polling).  A wait that exceeds it gives up, so a kernel always drains even

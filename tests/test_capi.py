@@ -64,9 +64,12 @@ def test_temp_bytes_queries(L):
     assert rc == 0 and b == 2048 * 4
     rc, b = _q(L.lcpp_reduce_temp_bytes, 5, 1 << 28)
     assert rc == 0 and b == 2048 * 8
-    # scan: ticket + one packed 64-bit word per 4096-element tile
+    # scan: one packed 64-bit word per 16384-element tile (two per 8192-element
+    # tile for 64-bit types)
     rc, b = _q(L.lcpp_scan_temp_bytes, 1, 1 << 28)
-    assert rc == 0 and b == 256 + (1 << 16) * 8
+    assert rc == 0 and b == (1 << 14) * 8
+    rc, b = _q(L.lcpp_scan_temp_bytes, 4, 1 << 27)
+    assert rc == 0 and b == (1 << 14) * 16
     # sort: bins + 2 regions of tile counts + 2 regions of batch words + key
     # scratch (no value scratch for keys-only); 16384-key tiles, batches of 8
     rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, 1 << 28)

@@ -40,7 +40,8 @@ def test_kat_ones_reused_temp(gpu):
 
 
 @pytest.mark.parametrize("dtype", INT_DTYPES)
-@pytest.mark.parametrize("n", [1, 2, 2047, 2048, 4095, 4096, 4097, 100_003, 1 << 20])
+# tiles hold 16384 32-bit / 8192 64-bit elements: cover both boundaries
+@pytest.mark.parametrize("n", [1, 2, 4097, 8191, 8192, 8193, 16383, 16384, 16385, 3 * 16384 + 5, 100_003, 1 << 20])
 @pytest.mark.parametrize("pad", [0, 1])
 def test_integers_vs_oracle(gpu, dtype, n, pad):
     import gpu_util as g
