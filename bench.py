@@ -26,6 +26,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "rs_onesweep_u32_2p28_hbm_bytes.txt")
+
+
+def measured_traffic():
+    """HBM bytes per onesweep launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (copy-calibrated), or None when that summary is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if "traffic_bytes_per_launch" in line:
+                    return int(line.split("=")[1].split()[0])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
 
 
 def parse():
@@ -36,6 +50,8 @@ def parse():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None, help="run one secondary workload by name (profiling)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 2^28 x uint32 streaming copy (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
 
 
@@ -89,6 +105,16 @@ def main():
     U32, F32, I32, U64 = 1, 2, 0, 4
     chk = lcpp._capi.check
 
+    if args.copy_probe:
+        n = 1 << 28
+        src = datagen.keys_u32(n)
+        dst = torch.empty_like(src)
+        ms = timed(lambda: datagen.copy_probe(src, dst), args.steps, args.warmup)
+        print(json.dumps({"copy_probe": {"bytes_read_per_launch": 4 * n, "bytes_written_per_launch": 4 * n,
+                                         "launches": args.steps + args.warmup, "ms": round(ms, 4),
+                                         "GB/s": round(8 * n / (ms * 1e-3) / 1e9, 1)}}), flush=True)
+        return
+
     # ------------------------------------------------------------ headline: SortKeys u32 2^28
     n = 1 << 28
     keys = datagen.keys_u32(n)
@@ -136,7 +162,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated: profiles/rs_onesweep_u32_2p28_hbm_bytes.txt",
             "bytes_per_launch": pass_bytes,
             "avg_launch_us": round(pass_ms * 1e3, 2),
             "launches": pass_launches,

@@ -71,9 +71,32 @@ int launch(void *out, uint64_t n, uint64_t s0, uint64_t s1, uint64_t s2, void *s
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
+// Plain streaming copy (16-byte loads and stores, grid-stride): a kernel of
+// known traffic (read 4n + write 4n bytes) against which hardware byte
+// counters (FETCH_SIZE / WRITE_SIZE) are calibrated.
+typedef uint32_t u32x4c __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void copy_probe_kernel(const u32x4c *__restrict__ in, u32x4c *__restrict__ out,
+                                                         uint64_t nvec)
+{
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += stride)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(in + i), out + i);
+}
+
 }  // namespace
 
 extern "C" {
+
+// n must be a multiple of 4 and both pointers 16-byte aligned.
+int lcpp_copy_probe_u32(const void *in, void *out, uint64_t n, void *stream)
+{
+    if (n == 0) return 0;
+    if (!in || !out || (n & 3) || ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15))
+        return -1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    copy_probe_kernel<<<8192, 256, 0, s>>>(static_cast<const u32x4c *>(in), static_cast<u32x4c *>(out), n / 4);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
 
 int lcpp_gen_reduce_i32(uint64_t seed, uint64_t n, void *out, void *stream)
 {

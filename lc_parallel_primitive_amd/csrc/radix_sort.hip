@@ -22,11 +22,14 @@
 //    non-zero bin.  It also zeroes the look-back state of pass 0.
 //  * launches 2..P+1 "rs_onesweep": one 16384-key tile (8192 for 8-byte keys
 //    or values) per 512-thread workgroup, keys staged in LDS.  No ticket:
-//    tiles are mapped from the workgroup id so that every 8 consecutive
-//    tiles run on one XCD (workgroups are dispatched round-robin over the 8
-//    XCDs), which lets that XCD's L2 merge the adjacent digit runs the 8
-//    tiles write; a tile only ever waits on tiles dispatched at most 63
-//    workgroups after it.  Ranking: keys are loaded wave-striped (lane l of
+//    tiles are mapped from the workgroup id so that every R consecutive
+//    tiles (R = 16 on a full MI355X) run on one XCD (workgroups are
+//    dispatched round-robin over the 8 XCDs), which lets that XCD's L2 merge
+//    the adjacent digit runs those tiles write (1, 8, 16, 32 tiles per run:
+//    751, 606, 529, 544 us per pass at 2^28).  A tile only ever waits on
+//    tiles dispatched at most 8R-1 workgroups after it, so R is chosen on the
+//    host such that 8R is at most half of the workgroups the device holds at
+//    once (R = 1 is plain dispatch order and always safe).  Ranking: keys are loaded wave-striped (lane l of
 //    wave w, item u -> key w*64*IPT + u*64 + l) so items in order u and lanes
 //    in order l are input order; a key's rank in its (wave, digit) is one
 //    returning LDS atomic add on the wave's counter for that digit.  gfx950
@@ -220,23 +223,24 @@ struct LbState {
     uint32_t *tcount_next, *bword_next;  // the other region, cleared for the next pass
 };
 
-// Workgroup -> tile: in every full group of 64 workgroups, b = 64q + 8j + x
-// (x = the XCD that b is dispatched to) processes tile 64q + 8x + j, so the 8
-// tiles 64q + 8x .. +7 run on XCD x.  A partial last group maps identically.
-__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t grid)
+// Workgroup -> tile with R = 2^log_run tiles per XCD run: in every full group
+// of 8R workgroups, b = 8Rq + 8j + x (x = the XCD that b is dispatched to)
+// processes tile 8Rq + Rx + j, so tiles 8Rq + Rx .. +R-1 run on XCD x.  A
+// partial last group maps identically.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t grid, uint32_t log_run)
 {
-    constexpr uint32_t kGroup = 64;
-    const uint32_t g = b / kGroup;
-    if ((g + 1) * kGroup > grid) return b;
-    const uint32_t r = b % kGroup;
-    return g * kGroup + (r % 8) * 8 + r / 8;
+    const uint32_t log_group = log_run + 3;
+    const uint32_t g = b >> log_group;
+    if ((g + 1) << log_group > grid) return b;
+    const uint32_t r = b & ((1u << log_group) - 1);
+    return (g << log_group) + ((r & 7) << log_run) + (r >> 3);
 }
 
 template <int IPT, class UK, class UV, int KIND, bool PAIRS>
 __global__ __launch_bounds__(kOsBlock) void rs_onesweep_kernel(
     const UK *__restrict__ kin, UK *__restrict__ kout, const UV *__restrict__ vin,
     UV *__restrict__ vout, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
-    LbState lb)
+    LbState lb, uint32_t log_run)
 {
     constexpr int TILE = kOsBlock * IPT;
     constexpr int WAVE_ITEMS = kWave * IPT;
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(kOsBlock) void rs_onesweep_kernel(
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
-    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x, log_run);
     const uint32_t base = tile * (uint32_t)TILE;
     const uint32_t valid = n - base < (uint32_t)TILE ? n - base : (uint32_t)TILE;
 
@@ -484,6 +488,19 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
                         kin, n, chunk, bins, tc[0], L.tc_words, bw[0], L.bw_words));
         LCPP_CHECK_LAUNCH();
     }
+    // XCD run length: 8R <= half the onesweep workgroups resident at once
+    static uint32_t log_run = 0xFFFFFFFFu;
+    if (log_run == 0xFFFFFFFFu) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void *>(&rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS>), kOsBlock,
+                0) != hipSuccess)
+            return LCPP_ERR_HIP;
+        const uint64_t resident = (uint64_t)(per_cu > 0 ? per_cu : 1) * (uint64_t)num_cus();
+        uint32_t lr = 0;
+        while (lr < 4 && (8ull << (lr + 1)) * 2 <= resident) ++lr;
+        log_run = lr;
+    }
     // ping-pong so that the last pass lands in the output and the input is preserved
     const UK *src_k = kin;
     const UV *src_v = vin;
@@ -495,7 +512,7 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         LCPP_LAUNCH("rs_onesweep", s,
                     (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
                         src_k, dst_k, src_v, dst_v, (uint32_t)n, (uint32_t)(p * kRadixBits),
-                        bins + p * kRadix, lb)));
+                        bins + p * kRadix, lb, log_run)));
         LCPP_CHECK_LAUNCH();
         src_k = dst_k;
         src_v = dst_v;

@@ -40,6 +40,8 @@ def lib() -> ctypes.CDLL:
         L.lcpp_gen_keys_u32_and3.argtypes = [u64, u64, u64, u64, vp, vp]
         L.lcpp_gen_iota_u32.restype = i
         L.lcpp_gen_iota_u32.argtypes = [u64, vp, vp]
+        L.lcpp_copy_probe_u32.restype = i
+        L.lcpp_copy_probe_u32.argtypes = [vp, vp, u64, vp]
         L.lcpp_gen_segments_host.restype = i
         L.lcpp_gen_segments_host.argtypes = [u64, u64, u64, u64, vp, vp]
         _lib = L
@@ -129,3 +131,11 @@ def segments(n_items: int, n_segments: int, seed_empty: int = SEED_SEG_EMPTY, se
     _run(lib().lcpp_gen_segments_host(seed_empty, seed_len, n_items, n_segments, b.ctypes.data, e.ctypes.data),
          "gen_segments_host")
     return b, e
+
+
+def copy_probe(src, dst):
+    """Streaming copy of a uint32 tensor (n % 4 == 0): calibration kernel for
+    the HBM byte counters."""
+    n = src.numel()
+    _run(lib().lcpp_copy_probe_u32(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), n, _stream()),
+         "copy_probe")
