@@ -203,17 +203,30 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
 }
 
 // ------------------------------------------------------------------ onesweep pass
+// LDS of one onesweep workgroup.  The sorted tile goes through LDS in two
+// halves (sorted positions [0, TILE/2) then [TILE/2, TILE)), so a 16384-key
+// tile needs 32 KB of staging and three workgroups fit a CU.
 template <int IPT, class UK, class UV>
 struct OnesweepSmem {
-    static constexpr int TILE = kOsBlock * IPT;
+    static constexpr int HALF = kOsBlock * IPT / 2;
     union {
-        UK keys[TILE];
-        UV vals[TILE];
+        UK keys[HALF];
+        UV vals[HALF];
     };
-    uint32_t cnt[kOsWaves][kRadix];  // per-wave digit counters, then wave prefixes
+    uint32_t cnt[kOsWaves][kRadix];  // per-wave digit counters, then wave bases in the sorted tile
     uint32_t goff[kRadix];           // output position of sorted tile position 0 of digit d
+    uint32_t total[kRadix];          // digit counts of this tile
+    uint32_t within[kRadix];         // digit counts of the earlier tiles of this batch
     uint32_t wsum[2][kRadix / kWave];
 };
+
+// Waves per SIMD the register allocation targets: 6 (three 512-thread
+// workgroups per CU) for keys-only passes, 4 (two) when values ride along.
+template <class UK, class UV, bool PAIRS>
+constexpr int os_waves_per_eu()
+{
+    return PAIRS ? 4 : 6;
+}
 
 // Look-back state of one pass: tcount[tiles][256] (tile digit counts,
 // written once) and bword[batches][256] (batch aggregate, then batch
@@ -236,14 +249,24 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t grid, uint32_t
     return (g << log_group) + ((r & 7) << log_run) + (r >> 3);
 }
 
+// 16-bit halves of the packed rank registers
+__device__ __forceinline__ uint32_t half16(uint32_t w, int hi) { return hi ? w >> 16 : w & 0xFFFFu; }
+__device__ __forceinline__ uint32_t set_half16(uint32_t w, int hi, uint32_t v)
+{
+    return hi ? (w & 0xFFFFu) | (v << 16) : (w & 0xFFFF0000u) | v;
+}
+
 template <int IPT, class UK, class UV, int KIND, bool PAIRS>
-__global__ __launch_bounds__(kOsBlock) void rs_onesweep_kernel(
-    const UK *__restrict__ kin, UK *__restrict__ kout, const UV *__restrict__ vin,
-    UV *__restrict__ vout, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
-    LbState lb, uint32_t log_run)
+__global__ __launch_bounds__(kOsBlock)
+__attribute__((amdgpu_waves_per_eu(os_waves_per_eu<UK, UV, PAIRS>(), os_waves_per_eu<UK, UV, PAIRS>())))
+void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const UV *__restrict__ vin,
+                        UV *__restrict__ vout, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
+                        LbState lb, uint32_t log_run)
 {
     constexpr int TILE = kOsBlock * IPT;
+    constexpr int HALF = TILE / 2;
     constexpr int WAVE_ITEMS = kWave * IPT;
+    static_assert(TILE <= 65536, "tile ranks are packed in 16 bits");
     __shared__ OnesweepSmem<IPT, UK, UV> sm;
 
     const uint32_t tid = threadIdx.x;
@@ -276,11 +299,23 @@ __global__ __launch_bounds__(kOsBlock) void rs_onesweep_kernel(
     }
     __syncthreads();  // counters zeroed
 
-    // ---- stable rank within (wave, digit): lane-ordered LDS atomics
-    uint32_t rank[IPT];
+    // ---- stable rank within (wave, digit): lane-ordered LDS atomics; two
+    // 16-bit ranks per register
+    uint32_t rank2[IPT / 2];
     uint32_t *cnt = sm.cnt[wave];
 #pragma unroll
-    for (int u = 0; u < IPT; ++u) rank[u] = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u], shift)], 1u);
+    for (int u = 0; u < IPT; u += 2) {
+        const uint32_t r0 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u], shift)], 1u);
+        const uint32_t r1 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u + 1], shift)], 1u);
+        rank2[u / 2] = r0 | (r1 << 16);
+        if ((u & 7) == 6) __builtin_amdgcn_sched_barrier(0);
+    }
+    // Opaque copies: the counter addresses are recomputed after the barrier
+    // (two VALU ops) instead of being kept live (one register per key).
+#pragma unroll
+    for (int u = 0; u < IPT; ++u) asm volatile("" : "+v"(tk[u]));
+#pragma unroll
+    for (int u = 0; u < IPT / 2; ++u) asm volatile("" : "+v"(rank2[u]));
     __syncthreads();
 
     // ---- threads 0..255 own digit d: tile counts, publish, clear next slots
@@ -299,6 +334,7 @@ __global__ __launch_bounds__(kOsBlock) void rs_onesweep_kernel(
         }
         if (d == kRadix - 1) total -= (uint32_t)TILE - valid;  // drop the pads
         st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], total | kLbPartial);
+        sm.total[d] = total;
         lb.tcount_next[(size_t)tile * kRadix + d] = 0;
         if (batch_last) lb.bword_next[(size_t)batch * kRadix + d] = 0;
     }
@@ -309,99 +345,112 @@ __global__ __launch_bounds__(kOsBlock) void rs_onesweep_kernel(
     }
     uint32_t gbase = 0;
     if (batch == 0) gbase = digit_excl_scan(owner ? bins[d] : 0u, sm.wsum[1]);
-
-    // ---- issue the within-batch count reads before the LDS scatter
-    uint32_t wb[kBatch - 1], bw0[kBatchWindow];
-#pragma unroll
-    for (int k = 0; k < kBatch - 1; ++k)
-        wb[k] = owner && (uint32_t)k < bpos ? ld_relaxed(&lb.tcount[(size_t)(tile - bpos + k) * kRadix + d]) : 0u;
-#pragma unroll
-    for (int k = 0; k < kBatchWindow; ++k)
-        bw0[k] = owner && (int64_t)batch - 1 - k >= 0 ? ld_relaxed(&lb.bword[(size_t)(batch - 1 - k) * kRadix + d])
-                                                      : kLbGlobal;
     __syncthreads();
 
-    // ---- scatter keys into LDS in sorted-tile order
+    // ---- tile ranks (repacked in place); first half of the sorted tile into LDS
 #pragma unroll
     for (int u = 0; u < IPT; ++u) {
         const uint32_t dd = digit_of<UK, KIND>(tk[u], shift);
-        rank[u] += sm.cnt[wave][dd];
-        sm.keys[rank[u]] = tk[u];
+        const uint32_t r = half16(rank2[u / 2], u & 1) + sm.cnt[wave][dd];
+        rank2[u / 2] = set_half16(rank2[u / 2], u & 1, r);
+        if (r < (uint32_t)HALF) sm.keys[r] = tk[u];
+        if ((u & 7) == 7) __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- two-level look-back for digit d
-    if (owner) {
+    // ---- two-level look-back.  Waves 4..7 read the counts of the earlier
+    // tiles of the batch (and the batch's last tile publishes the batch
+    // aggregate); waves 0..3 walk the earlier batch words.
+    if (!owner && tid < 2u * kRadix) {
+        const uint32_t d2 = tid - kRadix;
+        // branch-free polls: slots k >= bpos re-read this tile's own word
+        const uint32_t *tb = lb.tcount + (size_t)(tile - bpos) * kRadix + d2;
+        uint32_t w7[kBatch - 1];
+#pragma unroll
+        for (int k = 0; k < kBatch - 1; ++k) w7[k] = ld_relaxed(tb + ((uint32_t)k < bpos ? k : bpos) * kRadix);
         uint32_t within = 0;
 #pragma unroll
-        for (int k = 0; k < kBatch - 1; ++k) {
-            if ((uint32_t)k < bpos) {
-                const uint32_t w = wait_word(&lb.tcount[(size_t)(tile - bpos + k) * kRadix + d], wb[k]);
-                within += w & kLbMask;
-            }
-        }
+        for (int k = 0; k < kBatch - 1; ++k)
+            if ((uint32_t)k < bpos) within += wait_word(tb + k * kRadix, w7[k]) & kLbMask;
+        sm.within[d2] = within;
         if (batch_last && batch > 0)
-            st_relaxed(&lb.bword[(size_t)batch * kRadix + d], (within + total) | kLbPartial);
-        uint32_t bexcl;
-        if (batch == 0) {
-            bexcl = gbase;
-        } else {
-            uint32_t acc = 0;
-            int64_t j = (int64_t)batch - 1;
-            bool done = false;
-            bool first = true;
-            while (!done) {
-                uint32_t w[kBatchWindow];
+            st_relaxed(&lb.bword[(size_t)batch * kRadix + d2], (within + sm.total[d2]) | kLbPartial);
+    }
+    uint32_t bexcl = gbase;
+    if (owner && batch > 0) {
+        uint32_t acc = 0;
+        int64_t j = (int64_t)batch - 1;
+        bool done = false;
+        while (!done) {
+            uint32_t w[kBatchWindow];
 #pragma unroll
-                for (int k = 0; k < kBatchWindow; ++k)
-                    w[k] = first ? bw0[k] : j - k >= 0 ? ld_relaxed(&lb.bword[(size_t)(j - k) * kRadix + d]) : kLbGlobal;
-                first = false;
+            for (int k = 0; k < kBatchWindow; ++k) w[k] = ld_relaxed(&lb.bword[(size_t)(j - k >= 0 ? j - k : 0) * kRadix + d]);
 #pragma unroll
-                for (int k = 0; k < kBatchWindow; ++k) {
-                    if (!done) {
-                        const uint32_t wk =
-                            j - k >= 0 ? wait_word(&lb.bword[(size_t)(j - k) * kRadix + d], w[k]) : w[k];
-                        acc += wk & kLbMask;
-                        done = (wk & kLbGlobal) != 0;
-                    }
+            for (int k = 0; k < kBatchWindow; ++k) {
+                if (!done) {
+                    const uint32_t wk = j - k >= 0 ? wait_word(&lb.bword[(size_t)(j - k) * kRadix + d], w[k]) : kLbGlobal;
+                    acc += wk & kLbMask;
+                    done = (wk & kLbGlobal) != 0;
                 }
-                j -= kBatchWindow;
             }
-            bexcl = acc;
+            j -= kBatchWindow;
         }
+        bexcl = acc;
+    }
+    __syncthreads();
+    if (owner) {
+        const uint32_t within = sm.within[d];
         if (batch_last) st_relaxed(&lb.bword[(size_t)batch * kRadix + d], (bexcl + within + total) | kLbGlobal);
         sm.goff[d] = bexcl + within - dexcl;
     }
     __syncthreads();
 
-    // ---- write out: consecutive threads -> consecutive positions of a digit run
-    uint32_t dg[PAIRS ? IPT : 1];
+    // ---- write out, one half at a time: consecutive threads -> consecutive
+    // positions of a digit run; values follow with the same ranks
 #pragma unroll
-    for (int j = 0; j < IPT; ++j) {
-        const uint32_t i = j * kOsBlock + tid;
-        const UK k = sm.keys[i];
-        const uint32_t dd = digit_of<UK, KIND>(k, shift);
-        if constexpr (PAIRS) dg[j] = dd;
-        const uint32_t pos = i + sm.goff[dd];
-        if (i < valid && pos < n) kout[pos] = tw_out<UK, KIND>(k);
-    }
-    if constexpr (PAIRS) {
-        __syncthreads();
+    for (int h = 0; h < 2; ++h) {
+        if (h == 1) {
+            __syncthreads();  // first half written out
 #pragma unroll
-        for (int u = 0; u < IPT; ++u) sm.vals[rank[u]] = v[u];
-        __syncthreads();
+            for (int u = 0; u < IPT; ++u) {
+                const uint32_t r = half16(rank2[u / 2], u & 1);
+                if (r >= (uint32_t)HALF) sm.keys[r - HALF] = tk[u];
+                if ((u & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+            }
+            __syncthreads();
+        }
+        uint32_t pos[PAIRS ? IPT / 2 : 1];
 #pragma unroll
-        for (int j = 0; j < IPT; ++j) {
-            const uint32_t i = j * kOsBlock + tid;
-            const uint32_t pos = i + sm.goff[dg[j]];
-            if (i < valid && pos < n) vout[pos] = sm.vals[i];
+        for (int j = 0; j < IPT / 2; ++j) {
+            const uint32_t li = j * kOsBlock + tid;
+            const uint32_t i = h * HALF + li;
+            const UK k = sm.keys[li];
+            const uint32_t p = i + sm.goff[digit_of<UK, KIND>(k, shift)];
+            if constexpr (PAIRS) pos[j] = p;
+            if (i < valid && p < n) kout[p] = tw_out<UK, KIND>(k);
+            if ((j & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (PAIRS) {
+            __syncthreads();  // keys of this half read out
+#pragma unroll
+            for (int u = 0; u < IPT; ++u) {
+                const uint32_t r = half16(rank2[u / 2], u & 1);
+                if (r - h * HALF < (uint32_t)HALF) sm.vals[r - h * HALF] = v[u];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < IPT / 2; ++j) {
+                const uint32_t li = j * kOsBlock + tid;
+                const uint32_t i = h * HALF + li;
+                if (i < valid && pos[j] < n) vout[pos[j]] = sm.vals[li];
+            }
         }
     }
 }
 
 // ------------------------------------------------------------------ host side
 // Items per thread: 32 (16384-key tiles) when keys and values are 4 bytes,
-// 16 (8192-key tiles) when either is 8 bytes, so the LDS tile stays 64 KB
-// and two workgroups fit a CU.
+// 16 (8192-key tiles) when either is 8 bytes, so a half tile of either
+// stays 32 KB.
 constexpr int os_ipt(int key_bytes, int val_bytes) { return key_bytes == 8 || val_bytes == 8 ? 16 : 32; }
 
 struct RsLayout {
