@@ -175,7 +175,7 @@ class DeviceScan : public LuisaModule {
     }
 };
 
-/* device/device_radix_sort.h:37-153 */
+/* device/device_radix_sort.h:37-184 */
 template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
           size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
 class DeviceRadixSort : public LuisaModule {
@@ -211,6 +211,26 @@ class DeviceRadixSort : public LuisaModule {
         check(lcpp_radix_sort_keys(dtype_of<KeyType>(), temp_storage.data(), temp_storage.size_bytes(),
                                    d_keys_in.data(), d_keys_out.data(), num_items, cmdlist.stream),
               "DeviceRadixSort::SortKeys");
+    }
+    /* device/device_radix_sort.h:156-170 */
+    template <class KeyType, class ValueType>
+    void SortPairsDescending(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                             BufferView<KeyType> d_keys_out, BufferView<ValueType> d_values_in,
+                             BufferView<ValueType> d_values_out, uint num_items)
+    {
+        check(lcpp_radix_sort_pairs_descending(dtype_of<KeyType>(), dtype_of<ValueType>(), temp_storage.data(),
+                                               temp_storage.size_bytes(), d_keys_in.data(), d_keys_out.data(),
+                                               d_values_in.data(), d_values_out.data(), num_items, cmdlist.stream),
+              "DeviceRadixSort::SortPairsDescending");
+    }
+    /* device/device_radix_sort.h:172-184 */
+    template <class KeyType>
+    void SortKeysDescending(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                            BufferView<KeyType> d_keys_out, uint num_items)
+    {
+        check(lcpp_radix_sort_keys_descending(dtype_of<KeyType>(), temp_storage.data(), temp_storage.size_bytes(),
+                                              d_keys_in.data(), d_keys_out.data(), num_items, cmdlist.stream),
+              "DeviceRadixSort::SortKeysDescending");
     }
 };
 

@@ -87,7 +87,7 @@ int lcpp_scan_inclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const v
                             void *out, uint64_t n, void *stream);
 
 /* ---------------------------------------------------------------------
- * DeviceRadixSort (onesweep, ascending, all key bits) — device/device_radix_sort.h
+ * DeviceRadixSort (onesweep, all key bits) — device/device_radix_sort.h
  * Keys: any lcpp_dtype (signed and floating keys are bit-twiddled as in
  * common/util_type.h:98-175; -0.0 and +0.0 compare equal).  Values: any
  * lcpp_dtype (moved as raw 4- or 8-byte words).  n < 2^30.
@@ -105,6 +105,17 @@ int lcpp_radix_sort_pairs_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint64_t n, siz
 int lcpp_radix_sort_pairs(lcpp_dtype k, lcpp_dtype v, void *temp, size_t temp_bytes,
                           const void *keys_in, void *keys_out, const void *vals_in,
                           void *vals_out, uint64_t n, void *stream);
+/* replaces DeviceRadixSort::SortKeysDescending(cmdlist, temp, keys_in, keys_out, num_items),
+ * device_radix_sort.h:172-184: keys in non-increasing order (bit-inverted sort keys,
+ * RadixSortTwiddle<true>, agent/radix_rank_sort_operations.h:124-155).  Temp storage as for
+ * lcpp_radix_sort_keys_temp_bytes. */
+int lcpp_radix_sort_keys_descending(lcpp_dtype k, void *temp, size_t temp_bytes, const void *keys_in,
+                                    void *keys_out, uint64_t n, void *stream);
+/* replaces DeviceRadixSort::SortPairsDescending, device_radix_sort.h:156-170.  Stable: equal
+ * keys keep their input order.  Temp storage as for lcpp_radix_sort_pairs_temp_bytes. */
+int lcpp_radix_sort_pairs_descending(lcpp_dtype k, lcpp_dtype v, void *temp, size_t temp_bytes,
+                                     const void *keys_in, void *keys_out, const void *vals_in,
+                                     void *vals_out, uint64_t n, void *stream);
 
 /* ---------------------------------------------------------------------
  * DeviceSegmentReduce — device/device_segment_reduce.h

@@ -37,6 +37,8 @@ SIGNATURES = {
     "lcpp_radix_sort_keys": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
     "lcpp_radix_sort_pairs_temp_bytes": (_i, [_i, _i, _u64, _c_size_p]),
     "lcpp_radix_sort_pairs": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp, _u64, _vp]),
+    "lcpp_radix_sort_keys_descending": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
+    "lcpp_radix_sort_pairs_descending": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp, _u64, _vp]),
     "lcpp_segment_reduce_temp_bytes": (_i, [_i, _u64, _c_size_p]),
     "lcpp_segment_reduce_sum": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp, _vp, _vp]),
     "lcpp_profile_enable": (_i, [_i]),

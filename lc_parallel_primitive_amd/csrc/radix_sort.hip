@@ -1,17 +1,19 @@
-// radix_sort.hip — DeviceRadixSort::SortKeys/SortPairs (onesweep) for gfx950.
+// radix_sort.hip — DeviceRadixSort::SortKeys/SortPairs(Descending) (onesweep)
+// for gfx950.
 //
-// Reference: device/device_radix_sort.h:129-153, 187-378 (reset, histogram,
+// Reference: device/device_radix_sort.h:129-184, 187-378 (reset, histogram,
 // bin exclusive sum, then per pass x portion: look-back memset + onesweep),
 // agent/agent_radix_sort_histogram.h:45-198, agent/agent_radix_sort_onesweep.h
 // :43-500, block/block_radix_rank.h:66-336, agent/radix_rank_sort_operations.h,
 // common/util_type.h:98-175 (twiddles), common/utils.h:273-324 (MatchAny).
 //
 // MI355X design (HBM-bound integer/byte work, no MFMA).  Measured on the
-// device: a cross-workgroup publish is observed ~0.5 us later, and 65536
-// same-address atomics take ~0.75 ms.  The reference's shape (1024-key tiles,
-// a per-tile ticket, a per-digit walk over every earlier tile) therefore
-// cannot keep up at 8 TB/s: at the tile rate the pass needs, each tile would
-// walk ~100 predecessors per digit.  The pass here is built around that:
+// device: a cross-workgroup publish is observed ~0.5 us later (1.5-2 us under
+// full HBM load), and 65536 same-address atomics take ~0.75 ms.  The
+// reference's shape (1024-key tiles, a per-tile ticket, a per-digit walk over
+// every earlier tile) therefore cannot keep up at 8 TB/s: at the tile rate
+// the pass needs, each tile would walk ~100 predecessors per digit.  The pass
+// here is built around that:
 //
 //  * launch 0 "rs_init": zero the P digit histograms.
 //  * launch 1 "rs_histogram": one 1024-thread workgroup per CU streams a
@@ -21,35 +23,41 @@
 //    key bytes) never hit one LDS address; flushed with one global atomic per
 //    non-zero bin.  It also zeroes the look-back state of pass 0.
 //  * launches 2..P+1 "rs_onesweep": one 16384-key tile (8192 for 8-byte keys
-//    or values) per 512-thread workgroup, keys staged in LDS.  No ticket:
-//    tiles are mapped from the workgroup id so that every R consecutive
-//    tiles (R = 16 on a full MI355X) run on one XCD (workgroups are
-//    dispatched round-robin over the 8 XCDs), which lets that XCD's L2 merge
-//    the adjacent digit runs those tiles write (1, 8, 16, 32 tiles per run:
-//    751, 606, 529, 544 us per pass at 2^28).  A tile only ever waits on
-//    tiles dispatched at most 8R-1 workgroups after it, so R is chosen on the
-//    host such that 8R is at most half of the workgroups the device holds at
-//    once (R = 1 is plain dispatch order and always safe).  Ranking: keys are loaded wave-striped (lane l of
-//    wave w, item u -> key w*64*IPT + u*64 + l) so items in order u and lanes
-//    in order l are input order; a key's rank in its (wave, digit) is one
-//    returning LDS atomic add on the wave's counter for that digit.  gfx950
-//    serves same-address LDS atomics of one instruction in lane order, so
-//    the ranks are stable (an in-bounds probe found no exception in 5e8
-//    lane-operations over uniform, skewed and constant digits; the parity
-//    tests check stability on every run).
+//    or values) per 512-thread workgroup.  No ticket: tiles are mapped from
+//    the workgroup id so that every R consecutive tiles (R = 16 on a full
+//    MI355X) run on one XCD (workgroups are dispatched round-robin over the 8
+//    XCDs), which lets that XCD's L2 merge the adjacent digit runs those
+//    tiles write (1, 8, 16, 32 tiles per run: 751, 606, 529, 544 us per pass
+//    at 2^28).  A tile only ever waits on tiles dispatched at most 8R-1
+//    workgroups after it, so R is chosen on the host such that 8R is at most
+//    half of the workgroups the device holds at once (R = 1 is plain
+//    dispatch order and always safe).
+//  * Ranking: keys are loaded wave-striped (lane l of wave w, item u -> key
+//    w*64*IPT + u*64 + l) so items in order u and lanes in order l are input
+//    order; a key's rank in its (wave, digit) is one returning LDS atomic add
+//    on the wave's counter for that digit.  gfx950 serves same-address LDS
+//    atomics of one instruction in lane order, so the ranks are stable (an
+//    in-bounds probe found no exception in 5e8 lane-operations over uniform,
+//    skewed and constant digits; the parity tests check stability on every
+//    run).  Ranks are kept two per register (16 bits each).
 //  * Two-level decoupled look-back.  Tiles form batches of 8.  Each tile
 //    publishes its 256 digit counts once.  A tile's exclusive prefix = the
 //    exclusive prefix of its batch + the counts of the earlier tiles of its
-//    batch (at most 7 parallel reads per digit).  The last tile of a batch
-//    publishes the batch aggregate (PARTIAL) as soon as it has its
-//    batch-mates' counts and the batch's inclusive prefix (GLOBAL) after a
-//    windowed walk over earlier batch words.  Every wait is on an earlier
-//    tile.  Words are 32-bit {GLOBAL:1 | PARTIAL:1 | value:30}, accessed
-//    with agent-scope atomics (the 8 XCD L2s are not coherent).  Two look-back
-//    regions alternate between passes and each tile clears its own slots of
-//    the other region for the next pass (no per-pass memset launch).
-//  * Keys leave LDS in sorted order: consecutive threads write consecutive
-//    positions of each digit run.  Values follow with the same ranks.
+//    batch (at most 7 parallel reads per digit, by waves 4..7).  The last
+//    tile of a batch publishes the batch aggregate (PARTIAL) as soon as it
+//    has its batch-mates' counts, and the batch's inclusive prefix (GLOBAL)
+//    after a windowed walk over earlier batch words (waves 0..3).  Every
+//    wait is on an earlier tile.  Words are 32-bit {GLOBAL:1 | PARTIAL:1 |
+//    value:30}, accessed with agent-scope atomics (the 8 XCD L2s are not
+//    coherent).  Two look-back regions alternate between passes and each tile
+//    clears its own slots of the other region for the next pass (no per-pass
+//    memset launch).
+//  * The sorted tile leaves through LDS in two halves (32 KB of staging
+//    instead of 64 KB), which lets keys-only passes run three workgroups per
+//    CU: consecutive threads write consecutive positions of each digit run.
+//    Values follow with the same ranks.
+//  * Descending order sorts the bit-inverted sort keys (one XOR in, one out),
+//    as RadixSortTwiddle<true> does; equal keys keep their input order.
 //  * Keys-only sorts reserve no value scratch (the reference reserves N
 //    values it never uses, device_radix_sort.h:118-122).
 #include "common.hpp"
@@ -88,15 +96,19 @@ __device__ __forceinline__ UK tw_out(UK k)
     else if constexpr (KIND == kFloat) return (k & high) ? UK(k ^ high) : UK(~k);
     else return k;
 }
-// Digit of a twiddled key; -0.0 is folded onto +0.0
-// (agent/radix_rank_sort_operations.h:33-62, ProcessFloatMinusZero).
+// Digit of a sort key.  Sort keys are twiddled keys XOR `flip` (0 for
+// ascending, all ones for descending: RadixSortTwiddle::In,
+// agent/radix_rank_sort_operations.h:124-155).  -0.0 and +0.0 are given the
+// same digits (radix_rank_sort_operations.h:33-62, ProcessFloatMinusZero);
+// their two sort keys are adjacent, so folding either onto the other yields
+// the same stable order.
 template <class UK, int KIND>
-__device__ __forceinline__ uint32_t digit_of(UK tk, uint32_t shift)
+__device__ __forceinline__ uint32_t digit_of(UK tk, uint32_t shift, UK flip)
 {
     if constexpr (KIND == kFloat) {
         constexpr UK high = UK(1) << (sizeof(UK) * 8 - 1);
-        constexpr UK minus_zero = UK(~high);  // tw_in(-0.0)
-        if (tk == minus_zero) tk = high;      // tw_in(+0.0)
+        const UK minus_zero = UK(~high) ^ flip;  // tw_in(-0.0) ^ flip
+        if (tk == minus_zero) tk = high ^ flip;  // tw_in(+0.0) ^ flip
     }
     return (uint32_t)(tk >> shift) & (kRadix - 1);
 }
@@ -150,7 +162,7 @@ template <class UK, int KIND>
 __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     const UK *__restrict__ keys, uint64_t n, uint64_t chunk, uint32_t *__restrict__ bins,
     uint32_t *__restrict__ clear0, uint64_t clear0_words, uint32_t *__restrict__ clear1,
-    uint64_t clear1_words)
+    uint64_t clear1_words, UK flip)
 {
     constexpr int P = sizeof(UK);
     constexpr int C = hist_copies<UK>();
@@ -163,10 +175,10 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     const uint64_t b0 = (uint64_t)blockIdx.x * chunk;
     const uint64_t b1 = b0 + chunk < n ? b0 + chunk : n;
     auto count = [&](UK raw) {
-        const UK tk = tw_in<UK, KIND>(raw);
+        const UK tk = tw_in<UK, KIND>(raw) ^ flip;
 #pragma unroll
         for (int p = 0; p < P; ++p)
-            atomicAdd(&s_hist[((uint32_t)p * kRadix + digit_of<UK, KIND>(tk, p * kRadixBits)) * C + copy], 1u);
+            atomicAdd(&s_hist[((uint32_t)p * kRadix + digit_of<UK, KIND>(tk, p * kRadixBits, flip)) * C + copy], 1u);
     };
     constexpr uint64_t V = 16 / sizeof(UK);
     constexpr int kVecs = 4;
@@ -261,7 +273,7 @@ __global__ __launch_bounds__(kOsBlock)
 __attribute__((amdgpu_waves_per_eu(os_waves_per_eu<UK, UV, PAIRS>(), os_waves_per_eu<UK, UV, PAIRS>())))
 void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const UV *__restrict__ vin,
                         UV *__restrict__ vout, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
-                        LbState lb, uint32_t log_run)
+                        LbState lb, uint32_t log_run, UK flip)
 {
     constexpr int TILE = kOsBlock * IPT;
     constexpr int HALF = TILE / 2;
@@ -284,7 +296,7 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     const uint32_t wbase = base + wave * WAVE_ITEMS + lane;
     if (valid == (uint32_t)TILE) {
 #pragma unroll
-        for (int u = 0; u < IPT; ++u) tk[u] = tw_in<UK, KIND>(__builtin_nontemporal_load(kin + wbase + u * kWave));
+        for (int u = 0; u < IPT; ++u) tk[u] = tw_in<UK, KIND>(__builtin_nontemporal_load(kin + wbase + u * kWave)) ^ flip;
         if constexpr (PAIRS) {
 #pragma unroll
             for (int u = 0; u < IPT; ++u) v[u] = __builtin_nontemporal_load(vin + wbase + u * kWave);
@@ -293,7 +305,7 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
 #pragma unroll
         for (int u = 0; u < IPT; ++u) {
             const uint32_t idx = wbase + u * kWave;
-            tk[u] = idx < n ? tw_in<UK, KIND>(kin[idx]) : UK(~UK(0));
+            tk[u] = idx < n ? UK(tw_in<UK, KIND>(kin[idx]) ^ flip) : UK(~UK(0));
             if constexpr (PAIRS) v[u] = idx < n ? vin[idx] : UV(0);
         }
     }
@@ -305,8 +317,8 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     uint32_t *cnt = sm.cnt[wave];
 #pragma unroll
     for (int u = 0; u < IPT; u += 2) {
-        const uint32_t r0 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u], shift)], 1u);
-        const uint32_t r1 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u + 1], shift)], 1u);
+        const uint32_t r0 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u], shift, flip)], 1u);
+        const uint32_t r1 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u + 1], shift, flip)], 1u);
         rank2[u / 2] = r0 | (r1 << 16);
         if ((u & 7) == 6) __builtin_amdgcn_sched_barrier(0);
     }
@@ -350,7 +362,7 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     // ---- tile ranks (repacked in place); first half of the sorted tile into LDS
 #pragma unroll
     for (int u = 0; u < IPT; ++u) {
-        const uint32_t dd = digit_of<UK, KIND>(tk[u], shift);
+        const uint32_t dd = digit_of<UK, KIND>(tk[u], shift, flip);
         const uint32_t r = half16(rank2[u / 2], u & 1) + sm.cnt[wave][dd];
         rank2[u / 2] = set_half16(rank2[u / 2], u & 1, r);
         if (r < (uint32_t)HALF) sm.keys[r] = tk[u];
@@ -424,9 +436,9 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
             const uint32_t li = j * kOsBlock + tid;
             const uint32_t i = h * HALF + li;
             const UK k = sm.keys[li];
-            const uint32_t p = i + sm.goff[digit_of<UK, KIND>(k, shift)];
+            const uint32_t p = i + sm.goff[digit_of<UK, KIND>(k, shift, flip)];
             if constexpr (PAIRS) pos[j] = p;
-            if (i < valid && p < n) kout[p] = tw_out<UK, KIND>(k);
+            if (i < valid && p < n) kout[p] = tw_out<UK, KIND>(UK(k ^ flip));
             if ((j & 7) == 7) __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (PAIRS) {
@@ -491,8 +503,9 @@ int num_cus()
 
 template <class UK, class UV, int KIND, bool PAIRS>
 int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const void *vin_,
-           void *vout_, uint64_t n, hipStream_t s)
+           void *vout_, uint64_t n, bool descending, hipStream_t s)
 {
+    const UK flip = descending ? UK(~UK(0)) : UK(0);
     constexpr int IPT = os_ipt(sizeof(UK), PAIRS ? sizeof(UV) : 0);
     if (n == 0) return LCPP_OK;
     if (n > kMaxItems) return LCPP_ERR_INVALID_ARG;
@@ -534,7 +547,7 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         grid = ceil_div(n, chunk);
         LCPP_LAUNCH("rs_histogram", s,
                     rs_histogram_kernel<UK, KIND><<<(uint32_t)grid, kHistBlock, lds, s>>>(
-                        kin, n, chunk, bins, tc[0], L.tc_words, bw[0], L.bw_words));
+                        kin, n, chunk, bins, tc[0], L.tc_words, bw[0], L.bw_words, flip));
         LCPP_CHECK_LAUNCH();
     }
     // XCD run length: 8R <= half the onesweep workgroups resident at once
@@ -561,7 +574,7 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         LCPP_LAUNCH("rs_onesweep", s,
                     (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
                         src_k, dst_k, src_v, dst_v, (uint32_t)n, (uint32_t)(p * kRadixBits),
-                        bins + p * kRadix, lb, log_run)));
+                        bins + p * kRadix, lb, log_run, flip)));
         LCPP_CHECK_LAUNCH();
         src_k = dst_k;
         src_v = dst_v;
@@ -589,12 +602,12 @@ int dtype_bytes(lcpp_dtype t)
 
 template <class UK, class UV, bool PAIRS>
 int rs_kind_dispatch(int kind, void *temp, size_t tb, const void *ki, void *ko, const void *vi,
-                     void *vo, uint64_t n, hipStream_t s)
+                     void *vo, uint64_t n, bool desc, hipStream_t s)
 {
     switch (kind) {
-    case kUnsigned: return rs_run<UK, UV, kUnsigned, PAIRS>(temp, tb, ki, ko, vi, vo, n, s);
-    case kSigned: return rs_run<UK, UV, kSigned, PAIRS>(temp, tb, ki, ko, vi, vo, n, s);
-    case kFloat: return rs_run<UK, UV, kFloat, PAIRS>(temp, tb, ki, ko, vi, vo, n, s);
+    case kUnsigned: return rs_run<UK, UV, kUnsigned, PAIRS>(temp, tb, ki, ko, vi, vo, n, desc, s);
+    case kSigned: return rs_run<UK, UV, kSigned, PAIRS>(temp, tb, ki, ko, vi, vo, n, desc, s);
+    case kFloat: return rs_run<UK, UV, kFloat, PAIRS>(temp, tb, ki, ko, vi, vo, n, desc, s);
     default: return LCPP_ERR_UNSUPPORTED_DTYPE;
     }
 }
@@ -623,30 +636,63 @@ extern "C" int lcpp_radix_sort_pairs_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint
     return LCPP_OK;
 }
 
-extern "C" int lcpp_radix_sort_keys(lcpp_dtype k, void *temp, size_t tb, const void *keys_in,
-                                    void *keys_out, uint64_t n, void *stream)
+namespace {
+int sort_keys(lcpp_dtype k, void *temp, size_t tb, const void *keys_in, void *keys_out, uint64_t n,
+              bool desc, void *stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int kind = key_kind(k);
     if (kind < 0) return LCPP_ERR_UNSUPPORTED_DTYPE;
     if (dtype_bytes(k) == 4)
-        return rs_kind_dispatch<uint32_t, uint32_t, false>(kind, temp, tb, keys_in, keys_out, nullptr, nullptr, n, s);
-    return rs_kind_dispatch<uint64_t, uint32_t, false>(kind, temp, tb, keys_in, keys_out, nullptr, nullptr, n, s);
+        return rs_kind_dispatch<uint32_t, uint32_t, false>(kind, temp, tb, keys_in, keys_out, nullptr, nullptr, n,
+                                                           desc, s);
+    return rs_kind_dispatch<uint64_t, uint32_t, false>(kind, temp, tb, keys_in, keys_out, nullptr, nullptr, n,
+                                                       desc, s);
 }
 
-extern "C" int lcpp_radix_sort_pairs(lcpp_dtype k, lcpp_dtype v, void *temp, size_t tb,
-                                     const void *keys_in, void *keys_out, const void *vals_in,
-                                     void *vals_out, uint64_t n, void *stream)
+int sort_pairs(lcpp_dtype k, lcpp_dtype v, void *temp, size_t tb, const void *keys_in, void *keys_out,
+               const void *vals_in, void *vals_out, uint64_t n, bool desc, void *stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int kind = key_kind(k);
     const int kb = dtype_bytes(k), vb = dtype_bytes(v);
     if (kind < 0 || !vb) return LCPP_ERR_UNSUPPORTED_DTYPE;
     if (kb == 4 && vb == 4)
-        return rs_kind_dispatch<uint32_t, uint32_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n, s);
+        return rs_kind_dispatch<uint32_t, uint32_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
+                                                          desc, s);
     if (kb == 4 && vb == 8)
-        return rs_kind_dispatch<uint32_t, uint64_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n, s);
+        return rs_kind_dispatch<uint32_t, uint64_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
+                                                          desc, s);
     if (kb == 8 && vb == 4)
-        return rs_kind_dispatch<uint64_t, uint32_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n, s);
-    return rs_kind_dispatch<uint64_t, uint64_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n, s);
+        return rs_kind_dispatch<uint64_t, uint32_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
+                                                          desc, s);
+    return rs_kind_dispatch<uint64_t, uint64_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
+                                                      desc, s);
+}
+}  // namespace
+
+extern "C" int lcpp_radix_sort_keys(lcpp_dtype k, void *temp, size_t tb, const void *keys_in,
+                                    void *keys_out, uint64_t n, void *stream)
+{
+    return sort_keys(k, temp, tb, keys_in, keys_out, n, false, stream);
+}
+
+extern "C" int lcpp_radix_sort_pairs(lcpp_dtype k, lcpp_dtype v, void *temp, size_t tb,
+                                     const void *keys_in, void *keys_out, const void *vals_in,
+                                     void *vals_out, uint64_t n, void *stream)
+{
+    return sort_pairs(k, v, temp, tb, keys_in, keys_out, vals_in, vals_out, n, false, stream);
+}
+
+extern "C" int lcpp_radix_sort_keys_descending(lcpp_dtype k, void *temp, size_t tb, const void *keys_in,
+                                               void *keys_out, uint64_t n, void *stream)
+{
+    return sort_keys(k, temp, tb, keys_in, keys_out, n, true, stream);
+}
+
+extern "C" int lcpp_radix_sort_pairs_descending(lcpp_dtype k, lcpp_dtype v, void *temp, size_t tb,
+                                                const void *keys_in, void *keys_out, const void *vals_in,
+                                                void *vals_out, uint64_t n, void *stream)
+{
+    return sort_pairs(k, v, temp, tb, keys_in, keys_out, vals_in, vals_out, n, true, stream);
 }

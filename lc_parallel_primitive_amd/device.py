@@ -116,7 +116,7 @@ class DeviceScan:
 
 
 class DeviceRadixSort:
-    """device/device_radix_sort.h:37-153 (onesweep SortKeys / SortPairs, ascending)."""
+    """device/device_radix_sort.h:37-184 (onesweep SortKeys / SortPairs, ascending and descending)."""
 
     def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
         self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
@@ -133,28 +133,42 @@ class DeviceRadixSort:
         return _query(lib().lcpp_radix_sort_pairs_temp_bytes, dtype_code(key_dtype), dtype_code(value_dtype),
                       num_items)
 
-    def SortKeys(self, temp_storage, d_keys_in, d_keys_out, num_items: int, stream=None):
+    def _keys(self, fn, name, temp_storage, d_keys_in, d_keys_out, num_items, stream):
         _need(d_keys_in, num_items, "d_keys_in")
         _need(d_keys_out, num_items, "d_keys_out")
-        _same_dtype(d_keys_in, d_keys_out, "SortKeys")
-        L = lib()
-        check(L.lcpp_radix_sort_keys(dtype_code(d_keys_in.dtype), _ptr(temp_storage), _nbytes(temp_storage),
-                                     _ptr(d_keys_in), _ptr(d_keys_out), num_items, _stream(stream)),
-              "lcpp_radix_sort_keys")
+        _same_dtype(d_keys_in, d_keys_out, name)
+        check(fn(dtype_code(d_keys_in.dtype), _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_keys_in),
+                 _ptr(d_keys_out), num_items, _stream(stream)), name)
 
-    def SortPairs(self, temp_storage, d_keys_in, d_keys_out, d_values_in, d_values_out, num_items: int,
-                  stream=None):
+    def _pairs(self, fn, name, temp_storage, d_keys_in, d_keys_out, d_values_in, d_values_out, num_items, stream):
         for t, nm in ((d_keys_in, "d_keys_in"), (d_keys_out, "d_keys_out"), (d_values_in, "d_values_in"),
                       (d_values_out, "d_values_out")):
             _need(t, num_items, nm)
-        _same_dtype(d_keys_in, d_keys_out, "SortPairs keys")
-        _same_dtype(d_values_in, d_values_out, "SortPairs values")
-        L = lib()
-        check(L.lcpp_radix_sort_pairs(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype),
-                                      _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_keys_in),
-                                      _ptr(d_keys_out), _ptr(d_values_in), _ptr(d_values_out), num_items,
-                                      _stream(stream)),
-              "lcpp_radix_sort_pairs")
+        _same_dtype(d_keys_in, d_keys_out, name + " keys")
+        _same_dtype(d_values_in, d_values_out, name + " values")
+        check(fn(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype), _ptr(temp_storage),
+                 _nbytes(temp_storage), _ptr(d_keys_in), _ptr(d_keys_out), _ptr(d_values_in), _ptr(d_values_out),
+                 num_items, _stream(stream)), name)
+
+    def SortKeys(self, temp_storage, d_keys_in, d_keys_out, num_items: int, stream=None):
+        self._keys(lib().lcpp_radix_sort_keys, "lcpp_radix_sort_keys", temp_storage, d_keys_in, d_keys_out,
+                   num_items, stream)
+
+    def SortPairs(self, temp_storage, d_keys_in, d_keys_out, d_values_in, d_values_out, num_items: int,
+                  stream=None):
+        self._pairs(lib().lcpp_radix_sort_pairs, "lcpp_radix_sort_pairs", temp_storage, d_keys_in, d_keys_out,
+                    d_values_in, d_values_out, num_items, stream)
+
+    def SortKeysDescending(self, temp_storage, d_keys_in, d_keys_out, num_items: int, stream=None):
+        """device_radix_sort.h:172-184"""
+        self._keys(lib().lcpp_radix_sort_keys_descending, "lcpp_radix_sort_keys_descending", temp_storage,
+                   d_keys_in, d_keys_out, num_items, stream)
+
+    def SortPairsDescending(self, temp_storage, d_keys_in, d_keys_out, d_values_in, d_values_out,
+                            num_items: int, stream=None):
+        """device_radix_sort.h:156-170 (stable: equal keys keep input order)"""
+        self._pairs(lib().lcpp_radix_sort_pairs_descending, "lcpp_radix_sort_pairs_descending", temp_storage,
+                    d_keys_in, d_keys_out, d_values_in, d_values_out, num_items, stream)
 
 
 class DeviceSegmentReduce:

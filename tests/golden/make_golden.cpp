@@ -111,6 +111,18 @@ int main(int argc, char **argv)
         dump("sort_pairs_16384_vals_in_f32.bin", val);
         dump("sort_pairs_16384_keys_expect_u32.bin", ek);
         dump("sort_pairs_16384_vals_expect_f32.bin", ev);
+        // SortPairsDescending on the second stream (:220-231, 244-248)
+        std::vector<std::pair<uint32_t, float>> dkv(n);
+        for (int i = 0; i < n; ++i) dkv[i] = {dkey[i], dval[i]};
+        std::sort(dkv.begin(), dkv.end(), [](auto &a, auto &b) { return a.first > b.first; });
+        for (int i = 0; i < n; ++i) {
+            ek[i] = dkv[i].first;
+            ev[i] = dkv[i].second;
+        }
+        dump("sort_pairs_desc_16384_keys_in_u32.bin", dkey);
+        dump("sort_pairs_desc_16384_vals_in_f32.bin", dval);
+        dump("sort_pairs_desc_16384_keys_expect_u32.bin", ek);
+        dump("sort_pairs_desc_16384_vals_expect_f32.bin", ev);
     }
     return 0;
 }

@@ -28,6 +28,10 @@ MANIFEST = {
         "sort_pairs_16384_vals_in_f32.bin": ["float32", "device_radix_sort_one_sweep.cpp:155-175 values"],
         "sort_pairs_16384_keys_expect_u32.bin": ["uint32", "std::sort by key"],
         "sort_pairs_16384_vals_expect_f32.bin": ["float32", "values in key order"],
+        "sort_pairs_desc_16384_keys_in_u32.bin": ["uint32", "device_radix_sort_one_sweep.cpp:155-175 second keys, n=16384"],
+        "sort_pairs_desc_16384_vals_in_f32.bin": ["float32", "device_radix_sort_one_sweep.cpp:155-175 second values"],
+        "sort_pairs_desc_16384_keys_expect_u32.bin": ["uint32", "std::sort by key, greater"],
+        "sort_pairs_desc_16384_vals_expect_f32.bin": ["float32", "values in descending key order"],
     },
 }
 for n in (32, 256, 4096):

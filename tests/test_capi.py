@@ -90,6 +90,9 @@ def test_unsupported_dtype_and_null_args(L):
     assert L.lcpp_scan_exclusive_sum(0, None, 0, None, None, 10, None) == -1
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 10, None) == -1
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 1 << 30, None) == -1  # n >= 2^30
+    assert L.lcpp_radix_sort_keys_descending(1, None, 0, None, None, 10, None) == -1
+    assert L.lcpp_radix_sort_pairs_descending(1, 9, None, 0, None, None, None, None, 10, None) == -3
+    assert L.lcpp_radix_sort_pairs_descending(4, 1, None, 0, None, None, None, None, 10, None) == -1
     assert L.lcpp_segment_reduce_sum(2, None, 0, None, None, 10, None, None, None) == -1
     # zero-sized work is a no-op success
     assert L.lcpp_scan_inclusive_sum(0, None, 0, None, None, 0, None) == 0

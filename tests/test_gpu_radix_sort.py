@@ -1,4 +1,4 @@
-"""DeviceRadixSort::SortKeys/SortPairs (onesweep) on the GPU through the C ABI.
+"""DeviceRadixSort::SortKeys/SortPairs(Descending) (onesweep) on the GPU through the C ABI.
 Bit-exact against the oracle (itself pinned against numpy stable sorts and
 the reference's known answers); pairs are checked for stability; full-size
 configurations use O(N) sortedness + multiset / stability checkers."""
@@ -14,24 +14,26 @@ KEY_DTYPES = [np.uint32, np.int32, np.float32, np.uint64, np.int64, np.float64]
 SIZES = [1, 2, 63, 64, 65, 4095, 4096, 4097, 8191, 100_003]
 
 
-def sort_keys(d_in, n, dtype, pad=0):
+def sort_keys(d_in, n, dtype, pad=0, descending=False):
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceRadixSort
 
     out = g.empty(n, dtype, pad=pad)
     tmp = g.temp(DeviceRadixSort.GetSortKeysTempStorageBytes(np.dtype(dtype).name, n))
-    DeviceRadixSort().SortKeys(tmp, d_in, out, n)
+    s = DeviceRadixSort()
+    (s.SortKeysDescending if descending else s.SortKeys)(tmp, d_in, out, n)
     return out
 
 
-def sort_pairs(dk, dv, n, kdt, vdt):
+def sort_pairs(dk, dv, n, kdt, vdt, descending=False):
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceRadixSort
 
     ko = g.empty(n, kdt)
     vo = g.empty(n, vdt)
     tmp = g.temp(DeviceRadixSort.GetSortPairsTempStorageBytes(np.dtype(kdt).name, np.dtype(vdt).name, n))
-    DeviceRadixSort().SortPairs(tmp, dk, ko, dv, vo, n)
+    s = DeviceRadixSort()
+    (s.SortPairsDescending if descending else s.SortPairs)(tmp, dk, ko, dv, vo, n)
     return ko, vo
 
 
@@ -53,12 +55,26 @@ def test_kat_reversed_keys(gpu):
 
 @pytest.mark.parametrize("n", [32, 256, 4096])
 def test_kat_float_keys_golden(gpu, n):
-    # device_radix_sort_one_sweep.cpp:61-118 (ascending half; descending is not part of this build)
+    # device_radix_sort_one_sweep.cpp:61-118 (SortKeys and SortKeysDescending)
     import gpu_util as g
 
     a = golden(f"sort_float_{n}_asc_in_f32.bin", np.float32)
     got = g.to_host(sort_keys(g.to_dev(a), n, np.float32))
     assert same_bits(got, golden(f"sort_float_{n}_asc_expect_f32.bin", np.float32))
+    a = golden(f"sort_float_{n}_desc_in_f32.bin", np.float32)
+    got = g.to_host(sort_keys(g.to_dev(a), n, np.float32, descending=True))
+    assert same_bits(got, golden(f"sort_float_{n}_desc_expect_f32.bin", np.float32))
+
+
+def test_kat_pairs_descending_golden(gpu):
+    # device_radix_sort_one_sweep.cpp:153-279, SortPairsDescending leg
+    import gpu_util as g
+
+    k = golden("sort_pairs_desc_16384_keys_in_u32.bin", np.uint32)
+    v = golden("sort_pairs_desc_16384_vals_in_f32.bin", np.float32)
+    ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), k.size, np.uint32, np.float32, descending=True)
+    assert same_bits(g.to_host(ko), golden("sort_pairs_desc_16384_keys_expect_u32.bin", np.uint32))
+    assert same_bits(g.to_host(vo), golden("sort_pairs_desc_16384_vals_expect_f32.bin", np.float32))
 
 
 def test_kat_pairs_golden(gpu):
@@ -101,6 +117,35 @@ def test_pairs_stable_vs_oracle(gpu, kdt, vdt, n):
     assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
 
 
+@pytest.mark.parametrize("dtype", KEY_DTYPES)
+@pytest.mark.parametrize("n", [1, 65, 4097, 16385, 100_003])
+def test_keys_descending_vs_oracle(gpu, dtype, n):
+    import gpu_util as g
+
+    a = g.random_array(dtype, n, seed=n + 1)
+    log(f"sort keys descending {np.dtype(dtype).name} n={n}")
+    d = g.to_dev(a)
+    got = g.to_host(sort_keys(d, n, dtype, descending=True))
+    assert same_bits(got, o.radix_sort(a, descending=True))
+    assert same_bits(g.to_host(d), a)
+
+
+@pytest.mark.parametrize("kdt,vdt", [(np.uint32, np.uint32), (np.uint64, np.uint32), (np.float32, np.uint32),
+                                     (np.int64, np.float64)])
+@pytest.mark.parametrize("n", [4097, 100_003])
+def test_pairs_descending_stable_vs_oracle(gpu, kdt, vdt, n):
+    import gpu_util as g
+
+    k = g.random_array(kdt, n, seed=5)
+    if np.dtype(kdt).kind in "iu":
+        k = k & np.array(0xFF, dtype=kdt)
+    v = np.arange(n, dtype=vdt)
+    log(f"sort pairs descending {np.dtype(kdt).name}/{np.dtype(vdt).name} n={n}")
+    ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, kdt, vdt, descending=True)
+    rk, rv = o.radix_sort(k, v, descending=True)
+    assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
+
+
 def test_low_entropy_keys(gpu):
     import gpu_util as g
     from lc_parallel_primitive_amd import datagen
@@ -138,3 +183,31 @@ def test_full_size_pairs_u64_index(gpu):
     v = datagen.iota_u32(n)
     ko, vo = sort_pairs(k, v, n, np.uint64, np.uint32)
     assert o.check_stable_pairs_u64_u32(g.to_host(k), g.to_host(ko), g.to_host(vo))
+
+
+def test_full_size_u32_descending(gpu):
+    # C3a input sorted with SortKeysDescending: the reversed output must be an
+    # ascending permutation of the input
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    log("sort keys u32 descending full 2^28")
+    d = datagen.keys_u32(n)
+    got = g.to_host(sort_keys(d, n, np.uint32, descending=True))
+    assert o.check_sorted_permutation_u32(g.to_host(d), np.ascontiguousarray(got[::-1]))
+
+
+def test_full_size_pairs_u64_descending(gpu):
+    # C4 input with SortPairsDescending: a stable descending sort of k is a
+    # stable ascending sort of ~k, which the O(N) stability checker verifies
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 27
+    log("sort pairs u64/u32 descending full 2^27")
+    k = datagen.keys_u64_low16(n)
+    v = datagen.iota_u32(n)
+    ko, vo = sort_pairs(k, v, n, np.uint64, np.uint32, descending=True)
+    hk = g.to_host(k)
+    assert o.check_stable_pairs_u64_u32(~hk, ~g.to_host(ko), g.to_host(vo))

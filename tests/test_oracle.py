@@ -187,6 +187,55 @@ def test_sort_kat_pairs_golden():
     assert (vo == golden("sort_pairs_16384_vals_expect_f32.bin", np.float32)).all()
 
 
+def stable_descending_perm(a: np.ndarray) -> np.ndarray:
+    """Permutation that sorts `a` into non-increasing order, equal keys in
+    input order (an independent construction: a stable ascending argsort of
+    the reversed array, reversed back)."""
+    n = a.size
+    return (n - 1 - np.argsort(a[::-1], kind="stable"))[::-1]
+
+
+@pytest.mark.parametrize("dt", SORT_DTYPES)
+def test_sort_keys_descending_vs_numpy(dt):
+    rng = np.random.default_rng(11)
+    n = 50_003
+    if np.issubdtype(dt, np.floating):
+        a = (rng.standard_normal(n) * 1e3).astype(dt)
+        a[::97] = 0.0
+        a[::89] = -0.0
+    else:
+        info = np.iinfo(dt)
+        a = rng.integers(info.min, info.max, size=n, dtype=dt, endpoint=True)
+        a[::50] = a[7]  # duplicates
+    got = o.radix_sort(a, descending=True, nthreads=3, tile_items=1024)
+    ref = a[stable_descending_perm(a)]
+    assert (got == ref).all()
+    if np.issubdtype(dt, np.floating):  # +-0 compare equal and keep input order
+        assert (np.signbit(a[a == 0]) == np.signbit(got[got == 0])).all()
+
+
+def test_stable_descending_perm_is_independent_of_the_oracle():
+    a = np.array([3, 1, 3, 2, 1, 3], dtype=np.uint32)
+    assert stable_descending_perm(a).tolist() == [0, 2, 5, 3, 1, 4]
+
+
+def test_sort_pairs_descending_stability():
+    k = o.gen("keys_u64_low16", 200_000, 8)
+    v = np.arange(k.size, dtype=np.uint32)
+    ko, vo = o.radix_sort(k, v, descending=True, nthreads=4, tile_items=2048)
+    perm = stable_descending_perm(k)
+    assert (vo == perm).all() and (ko == k[perm]).all()
+
+
+def test_sort_kat_pairs_descending_golden():
+    # device_radix_sort_one_sweep.cpp:153-279, SortPairsDescending leg
+    k = golden("sort_pairs_desc_16384_keys_in_u32.bin", np.uint32)
+    v = golden("sort_pairs_desc_16384_vals_in_f32.bin", np.float32)
+    ko, vo = o.radix_sort(k, v, descending=True, nthreads=2, tile_items=1024)
+    assert (ko == golden("sort_pairs_desc_16384_keys_expect_u32.bin", np.uint32)).all()
+    assert (vo == golden("sort_pairs_desc_16384_vals_expect_f32.bin", np.float32)).all()
+
+
 def test_sort_pairs_stability_vs_numpy_argsort():
     k = o.gen("keys_u64_low16", 300_000, 4)
     v = np.arange(k.size, dtype=np.uint32)
