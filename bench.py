@@ -201,7 +201,14 @@ def main():
             add("DeviceReduce::Sum int32 N=2^24 (configs[0])", 4 * n24 + 4,
                 lambda: chk(L.lcpp_reduce_sum(I32, ctypes.c_void_p(t1.data_ptr()), tb, ctypes.c_void_p(x.data_ptr()),
                                               ctypes.c_void_p(o1.data_ptr()), n24, sp), "reduce"), 50, "reduce_partials")
-            del x, t1
+            ta = tmp_bytes(L.lcpp_reduce_arg_temp_bytes, I32, n)
+            t2 = torch.empty(max(ta, 1), dtype=torch.uint8, device="cuda")
+            ix = torch.empty(1, dtype=torch.int32, device="cuda")
+            add("DeviceReduce::ArgMin int32 N=2^28", 4 * n + 8,
+                lambda: chk(L.lcpp_reduce_argmin(I32, ctypes.c_void_p(t2.data_ptr()), ta,
+                                                 ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(o1.data_ptr()),
+                                                 ctypes.c_void_p(ix.data_ptr()), n, sp), "argmin"), 20, "arg_partials")
+            del x, t1, t2
         if want("scan"):
             n = 1 << 28
             x = datagen.u8_u32(n)

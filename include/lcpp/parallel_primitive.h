@@ -72,6 +72,37 @@ constexpr lcpp_dtype dtype_of()
     else static_assert(sizeof(U) == 0, "NumericT: 4- or 8-byte integer or floating type");
 }
 
+/* Reduction operators and element transforms TransformReduce can name.  The
+ * reference's SumOp / MinOp / MaxOp / IdentityOp are in
+ * common/thread_operators.h:49-80; its TransformReduce accepts any device
+ * functor, which a prebuilt library behind a C ABI cannot compile, so the set
+ * here is fixed (see lcpp_reduce_op / lcpp_transform). */
+struct SumOp {};
+struct MinOp {};
+struct MaxOp {};
+struct IdentityOp {};
+struct NegateOp {};
+struct AbsOp {};
+struct SquareOp {};
+
+template <class Op>
+constexpr lcpp_reduce_op reduce_op_of()
+{
+    if constexpr (std::is_same_v<Op, SumOp>) return LCPP_OP_SUM;
+    else if constexpr (std::is_same_v<Op, MinOp>) return LCPP_OP_MIN;
+    else if constexpr (std::is_same_v<Op, MaxOp>) return LCPP_OP_MAX;
+    else static_assert(sizeof(Op) == 0, "TransformReduce: reduce_op must be SumOp, MinOp or MaxOp");
+}
+template <class Xf>
+constexpr lcpp_transform transform_of()
+{
+    if constexpr (std::is_same_v<Xf, IdentityOp>) return LCPP_XFORM_IDENTITY;
+    else if constexpr (std::is_same_v<Xf, NegateOp>) return LCPP_XFORM_NEGATE;
+    else if constexpr (std::is_same_v<Xf, AbsOp>) return LCPP_XFORM_ABS;
+    else if constexpr (std::is_same_v<Xf, SquareOp>) return LCPP_XFORM_SQUARE;
+    else static_assert(sizeof(Xf) == 0, "TransformReduce: transform_op must be IdentityOp, NegateOp, AbsOp or SquareOp");
+}
+
 /* bytes -> count of uint words, as the reference's bytes_to_uint_count (common/utils.h:166-169) */
 inline size_t bytes_to_uint_count(size_t bytes) { return (bytes + sizeof(uint) - 1) / sizeof(uint); }
 
@@ -110,7 +141,7 @@ class LuisaModule {
     int m_last_status = LCPP_OK;
 };
 
-/* device/device_reduce.h:37-185 */
+/* device/device_reduce.h:37-348 */
 template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
           size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
 class DeviceReduce : public LuisaModule {
@@ -142,6 +173,42 @@ class DeviceReduce : public LuisaModule {
         check(lcpp_reduce_max(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
                               num_item, cmdlist.stream),
               "DeviceReduce::Max");
+    }
+    /* device/device_reduce.h:94-107 */
+    template <class T>
+    static size_t GetArgTempStorageBytes(size_t num_item)
+    {
+        size_t b = 0;
+        lcpp_reduce_arg_temp_bytes(dtype_of<T>(), num_item, &b);
+        return b;
+    }
+    /* device/device_reduce.h:187-227 */
+    template <class T>
+    void ArgMin(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, size_t num_item)
+    {
+        check(lcpp_reduce_argmin(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
+                                 d_out.data(), d_index_out.data(), num_item, cmdlist.stream),
+              "DeviceReduce::ArgMin");
+    }
+    /* device/device_reduce.h:229-272 */
+    template <class T>
+    void ArgMax(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, size_t num_item)
+    {
+        check(lcpp_reduce_argmax(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
+                                 d_out.data(), d_index_out.data(), num_item, cmdlist.stream),
+              "DeviceReduce::ArgMax");
+    }
+    /* device/device_reduce.h:331-348 */
+    template <class T, class ReduceOp, class TransformOp>
+    void TransformReduce(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                         size_t num_item, ReduceOp, TransformOp, T init)
+    {
+        check(lcpp_reduce_transform(dtype_of<T>(), reduce_op_of<ReduceOp>(), transform_of<TransformOp>(),
+                                    temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
+                                    num_item, &init, cmdlist.stream),
+              "DeviceReduce::TransformReduce");
     }
 };
 

@@ -44,6 +44,21 @@ typedef enum lcpp_dtype {
     LCPP_FLOAT64 = 5
 } lcpp_dtype;
 
+/* Reduction operators and element transforms of lcpp_reduce_transform (the
+ * reference takes arbitrary device functors; a C ABI carries a fixed set). */
+typedef enum lcpp_reduce_op {
+    LCPP_OP_SUM = 0,
+    LCPP_OP_MIN = 1,
+    LCPP_OP_MAX = 2
+} lcpp_reduce_op;
+
+typedef enum lcpp_transform {
+    LCPP_XFORM_IDENTITY = 0,
+    LCPP_XFORM_NEGATE = 1, /* integers wrap (two's complement) */
+    LCPP_XFORM_ABS = 2,    /* identity for unsigned types */
+    LCPP_XFORM_SQUARE = 3  /* integers wrap */
+} lcpp_transform;
+
 typedef enum lcpp_status {
     LCPP_OK = 0,
     LCPP_ERR_INVALID_ARG = -1,      /* null pointer, misaligned temp, size out of range */
@@ -73,6 +88,26 @@ int lcpp_reduce_min(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in,
  * uses numeric_limits<T>::min(), which differs for floating point only) */
 int lcpp_reduce_max(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
                     uint64_t n, void *stream);
+/* replaces DeviceReduce::TransformReduce(cmdlist, temp, d_in, d_out, num_item, reduce_op,
+ * transform_op, init), device_reduce.h:331-348:
+ * out[0] = op(init, op over i of xf(in[i])); *init is a host value of type t.
+ * Temp storage as for lcpp_reduce_temp_bytes. */
+int lcpp_reduce_transform(lcpp_dtype t, lcpp_reduce_op op, lcpp_transform xf, void *temp,
+                          size_t temp_bytes, const void *in, void *out, uint64_t n, const void *init,
+                          void *stream);
+/* replaces DeviceReduce::GetArgTempStorageBytes<T>(num_item), device_reduce.h:94-107 */
+int lcpp_reduce_arg_temp_bytes(lcpp_dtype t, uint64_t n, size_t *bytes);
+/* replaces DeviceReduce::ArgMin(cmdlist, temp, d_in, d_out, d_index_out, num_item),
+ * device_reduce.h:187-227: the smallest value and its index; ties go to the smallest index
+ * (ArgMinOp, common/thread_operators.h:34-47).  n = 0 gives (numeric max, 0xFFFFFFFF).
+ * n < 2^32. */
+int lcpp_reduce_argmin(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                       uint32_t *index_out, uint64_t n, void *stream);
+/* replaces DeviceReduce::ArgMax, device_reduce.h:229-272: the largest value and its index;
+ * ties go to the LARGEST index (ArgMaxOp, common/thread_operators.h:19-31).  Starts from
+ * numeric lowest() (the reference: numeric_limits<T>::min()), so n = 0 gives (lowest, 0). */
+int lcpp_reduce_argmax(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                       uint32_t *index_out, uint64_t n, void *stream);
 
 /* ---------------------------------------------------------------------
  * DeviceScan — device/device_scan.h

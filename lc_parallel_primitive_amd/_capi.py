@@ -9,6 +9,8 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 lib_path = os.path.join(_PKG, "liblcpp_amd.so")
 
 LCPP_INT32, LCPP_UINT32, LCPP_FLOAT32, LCPP_INT64, LCPP_UINT64, LCPP_FLOAT64 = range(6)
+LCPP_OPS = {"sum": 0, "min": 1, "max": 2}
+LCPP_TRANSFORMS = {"identity": 0, "negate": 1, "abs": 2, "square": 3}
 LCPP_DTYPES = {
     "int32": LCPP_INT32,
     "uint32": LCPP_UINT32,
@@ -30,6 +32,10 @@ SIGNATURES = {
     "lcpp_reduce_sum": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
     "lcpp_reduce_min": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
     "lcpp_reduce_max": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
+    "lcpp_reduce_transform": (_i, [_i, _i, _i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp, _vp]),
+    "lcpp_reduce_arg_temp_bytes": (_i, [_i, _u64, _c_size_p]),
+    "lcpp_reduce_argmin": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, _vp]),
+    "lcpp_reduce_argmax": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, _vp]),
     "lcpp_scan_temp_bytes": (_i, [_i, _u64, _c_size_p]),
     "lcpp_scan_exclusive_sum": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
     "lcpp_scan_inclusive_sum": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),

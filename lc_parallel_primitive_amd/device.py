@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import ctypes
 
-from ._capi import check, dtype_code, lib
+from ._capi import LCPP_OPS, LCPP_TRANSFORMS, check, dtype_code, lib
 
 
 def _ptr(t):
@@ -57,7 +57,7 @@ def _query(fn, *args) -> int:
 
 
 class DeviceReduce:
-    """device/device_reduce.h:37-185 (Sum / Min / Max)."""
+    """device/device_reduce.h:37-348 (Sum / Min / Max / ArgMin / ArgMax / TransformReduce)."""
 
     def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
         # geometry is fixed per dtype inside the library (tuned for gfx950);
@@ -86,6 +86,47 @@ class DeviceReduce:
 
     def Max(self, temp_storage, d_in, d_out, num_item: int, stream=None):
         self._run(lib().lcpp_reduce_max, temp_storage, d_in, d_out, num_item, stream)
+
+    @staticmethod
+    def GetArgTempStorageBytes(dtype, num_item: int) -> int:
+        return _query(lib().lcpp_reduce_arg_temp_bytes, dtype_code(dtype), num_item)
+
+    def _arg(self, fn, temp, d_in, d_out, d_index_out, num_item, stream):
+        _need(d_in, num_item, "d_in")
+        _need(d_out, 1, "d_out")
+        _need(d_index_out, 1, "d_index_out")
+        _same_dtype(d_in, d_out, fn.__name__)
+        if d_index_out.element_size() != 4:
+            raise TypeError(f"{fn.__name__}: d_index_out must hold 32-bit indices")
+        check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
+                 num_item, _stream(stream)), fn.__name__)
+
+    def ArgMin(self, temp_storage, d_in, d_out, d_index_out, num_item: int, stream=None):
+        """device_reduce.h:187-227: smallest value, ties to the smallest index."""
+        self._arg(lib().lcpp_reduce_argmin, temp_storage, d_in, d_out, d_index_out, num_item, stream)
+
+    def ArgMax(self, temp_storage, d_in, d_out, d_index_out, num_item: int, stream=None):
+        """device_reduce.h:229-272: largest value, ties to the largest index (ArgMaxOp)."""
+        self._arg(lib().lcpp_reduce_argmax, temp_storage, d_in, d_out, d_index_out, num_item, stream)
+
+    def TransformReduce(self, temp_storage, d_in, d_out, num_item: int, reduce_op: str, transform_op: str, init,
+                        stream=None):
+        """device_reduce.h:331-348: d_out[0] = reduce_op(init, reduce_op over i of transform_op(d_in[i])).
+        reduce_op: "sum" | "min" | "max"; transform_op: "identity" | "negate" | "abs" | "square"."""
+        import numpy as np
+
+        _need(d_in, num_item, "d_in")
+        _need(d_out, 1, "d_out")
+        _same_dtype(d_in, d_out, "TransformReduce")
+        if reduce_op not in LCPP_OPS or transform_op not in LCPP_TRANSFORMS:
+            raise ValueError(f"TransformReduce: unsupported ({reduce_op!r}, {transform_op!r})")
+        code = dtype_code(d_in.dtype)
+        np_dt = [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64][code]
+        iv = np.array([init], dtype=np_dt)
+        check(lib().lcpp_reduce_transform(code, LCPP_OPS[reduce_op], LCPP_TRANSFORMS[transform_op], _ptr(temp_storage),
+                                          _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), num_item,
+                                          ctypes.c_void_p(iv.ctypes.data), _stream(stream)),
+              "lcpp_reduce_transform")
 
 
 class DeviceScan:

@@ -233,6 +233,98 @@ int lcor_reduce_f64(int dtype, const void *in, uint64_t n, double *sum, double *
     return 0;
 }
 
+/* ======================================================================
+ * ArgMin / ArgMax — device/device_reduce.h:187-272 with ArgMinOp / ArgMaxOp
+ * (common/thread_operators.h:19-47): the running pair (value, index) is
+ * replaced by element i when its value is smaller (ArgMin) / larger (ArgMax),
+ * or equal with a smaller (ArgMin) / larger (ArgMax) index.  Init is
+ * (numeric max, 0xFFFFFFFF) for ArgMin (device_reduce.h:222-223) and
+ * (numeric lowest, 0) for ArgMax; the reference's ArgMax init is
+ * numeric_limits::min() (device_reduce.h:267), which differs from lowest()
+ * for floating point only (the GPU build uses lowest(), as the checker).
+ * ====================================================================== */
+#define ARG_FOLD(T, MAXV, LOWV)                                                        \
+    do {                                                                               \
+        const T *a = (const T *)in;                                                    \
+        T v = is_max ? (LOWV) : (MAXV);                                                \
+        uint32_t ix = is_max ? 0u : 0xFFFFFFFFu;                                       \
+        for (uint64_t i = 0; i < n; ++i) {                                             \
+            const T x = a[i];                                                          \
+            const uint32_t xi = (uint32_t)i;                                           \
+            const int take = is_max ? (x > v || (x == v && xi > ix))                   \
+                                    : (x < v || (x == v && xi < ix));                  \
+            if (take) { v = x; ix = xi; }                                              \
+        }                                                                              \
+        *(T *)out_value = v;                                                           \
+        *out_index = ix;                                                               \
+    } while (0)
+
+int lcor_reduce_arg(int is_max, int dtype, const void *in, uint64_t n, void *out_value, uint32_t *out_index)
+{
+    if (n > 0xFFFFFFFFull) return -1;
+    switch (dtype) {
+    case LCOR_I32: ARG_FOLD(int32_t, INT32_MAX, INT32_MIN); break;
+    case LCOR_U32: ARG_FOLD(uint32_t, UINT32_MAX, 0u); break;
+    case LCOR_F32: ARG_FOLD(float, 3.402823466e38f, -3.402823466e38f); break;
+    case LCOR_I64: ARG_FOLD(int64_t, INT64_MAX, INT64_MIN); break;
+    case LCOR_U64: ARG_FOLD(uint64_t, UINT64_MAX, 0u); break;
+    case LCOR_F64: ARG_FOLD(double, 1.7976931348623157e308, -1.7976931348623157e308); break;
+    default: return -1;
+    }
+    return 0;
+}
+
+/* ======================================================================
+ * TransformReduce — device/device_reduce.h:331-348 (reduce_array_recursive
+ * with a transform applied to every loaded item and `init` folded in):
+ * out = op(init, op over i of xf(in[i])), folded sequentially.  Integer
+ * transforms wrap (two's complement); |INT_MIN| = INT_MIN.
+ * ====================================================================== */
+#define XF_INT(T, U, SIGNED)                                                           \
+    static T xf_##T(int xf, T x)                                                       \
+    {                                                                                  \
+        switch (xf) {                                                                  \
+        case 1: return (T)((U)0 - (U)x);                                               \
+        case 2: return (SIGNED && ((U)x >> (sizeof(U) * 8 - 1))) ? (T)((U)0 - (U)x) : x; \
+        case 3: return (T)((U)x * (U)x);                                               \
+        default: return x;                                                             \
+        }                                                                              \
+    }
+XF_INT(int32_t, uint32_t, 1)
+XF_INT(uint32_t, uint32_t, 0)
+XF_INT(int64_t, uint64_t, 1)
+XF_INT(uint64_t, uint64_t, 0)
+static float xf_float(int xf, float x) { return xf == 1 ? -x : xf == 2 ? fabsf(x) : xf == 3 ? x * x : x; }
+static double xf_double(int xf, double x) { return xf == 1 ? -x : xf == 2 ? fabs(x) : xf == 3 ? x * x : x; }
+
+#define XFOLD(T, XFN, FOLD1)                                                           \
+    do {                                                                               \
+        const T *a = (const T *)in;                                                    \
+        T acc;                                                                         \
+        init_value(op, dtype, &acc);                                                   \
+        for (uint64_t i = 0; i < n; ++i) {                                             \
+            const T x = XFN(xf, a[i]);                                                 \
+            acc = FOLD1(op, &x, 1, acc);                                               \
+        }                                                                              \
+        const T iv = *(const T *)init;                                                 \
+        *(T *)out = FOLD1(op, &acc, 1, iv);                                            \
+    } while (0)
+
+int lcor_reduce_transform(int op, int xf, int dtype, const void *in, uint64_t n, const void *init, void *out)
+{
+    if (op < 0 || op > 2 || xf < 0 || xf > 3 || !init) return -1;
+    switch (dtype) {
+    case LCOR_I32: XFOLD(int32_t, xf_int32_t, fold_i32); break;
+    case LCOR_U32: XFOLD(uint32_t, xf_uint32_t, fold_u32); break;
+    case LCOR_F32: XFOLD(float, xf_float, fold_f32); break;
+    case LCOR_I64: XFOLD(int64_t, xf_int64_t, fold_i64); break;
+    case LCOR_U64: XFOLD(uint64_t, xf_uint64_t, fold_u64); break;
+    case LCOR_F64: XFOLD(double, xf_double, fold_f64); break;
+    default: return -1;
+    }
+    return 0;
+}
+
 /* ---------------- multithreaded reduce (CPU baseline) ----------------- */
 typedef struct {
     int op, dtype;

@@ -19,6 +19,11 @@
  *   generators      splitmix64 published test vector (Vigna, seed 1234567)
  *   reduce          Python big-int closed form, numpy min/max, reference KATs
  *                   (N ones -> N; shuffled 0..4095 -> 0 / 4095)
+ *   arg reduce      numpy argmin (first index) and reversed argmax (last
+ *                   index), reference KAT (shuffled 0..4095 -> positions of
+ *                   0 and 4095)
+ *   transform       numpy transforms + reductions in the element type,
+ *                   reference KAT (max of squares of shuffled 0..4095)
  *   scan            numpy cumsum in the element type (wraparound), KATs
  *                   (ones -> i / i+1), look-back KAT (102400 tiles)
  *   radix sort      numpy stable argsort/sort, reversed-keys KAT, float KAT
@@ -67,6 +72,10 @@ int lcor_gen_segments(uint64_t seed_empty, uint64_t seed_len, uint64_t n_items,
 int lcor_reduce(int op, int dtype, const void *in, uint64_t n, void *out);
 int lcor_reduce_f64(int dtype, const void *in, uint64_t n, double *sum, double *abs_sum);
 int lcor_reduce_mt(int op, int dtype, const void *in, uint64_t n, void *out, int nthreads);
+/* ArgMin (is_max = 0) / ArgMax (is_max = 1): value and 32-bit index */
+int lcor_reduce_arg(int is_max, int dtype, const void *in, uint64_t n, void *out_value, uint32_t *out_index);
+/* TransformReduce: out = op(init, op over i of xf(in[i])); xf 0 identity, 1 negate, 2 abs, 3 square */
+int lcor_reduce_transform(int op, int xf, int dtype, const void *in, uint64_t n, const void *init, void *out);
 
 /* ---------------- scan ------------------------------------------------- */
 int lcor_scan(int inclusive, int dtype, const void *in, void *out, uint64_t n);

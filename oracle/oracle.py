@@ -54,6 +54,8 @@ def lib() -> ctypes.CDLL:
             "lcor_reduce": (i, [i, i, vp, u64, vp]),
             "lcor_reduce_f64": (i, [i, vp, u64, vp, vp]),
             "lcor_reduce_mt": (i, [i, i, vp, u64, vp, i]),
+            "lcor_reduce_arg": (i, [i, i, vp, u64, vp, ctypes.POINTER(u32)]),
+            "lcor_reduce_transform": (i, [i, i, i, vp, u64, vp, vp]),
             "lcor_scan": (i, [i, i, vp, vp, u64]),
             "lcor_scan_f64": (i, [i, i, vp, vp, vp, u64]),
             "lcor_scan_mt": (i, [i, i, vp, vp, u64, i]),
@@ -133,6 +135,26 @@ def reduce(op: int, a: np.ndarray, nthreads: int = 1):
         _ok(lib().lcor_reduce(op, _code(a), _p(a), a.size, _p(out)), "reduce")
     else:
         _ok(lib().lcor_reduce_mt(op, _code(a), _p(a), a.size, _p(out), nthreads), "reduce_mt")
+    return out[0]
+
+
+def reduce_arg(is_max: bool, a: np.ndarray):
+    """(value, index) of ArgMax (is_max) / ArgMin."""
+    a = np.ascontiguousarray(a)
+    out = np.zeros(1, a.dtype)
+    idx = ctypes.c_uint32()
+    _ok(lib().lcor_reduce_arg(int(is_max), _code(a), _p(a), a.size, _p(out), ctypes.byref(idx)), "reduce_arg")
+    return out[0], idx.value
+
+
+XF_IDENTITY, XF_NEGATE, XF_ABS, XF_SQUARE = range(4)
+
+
+def reduce_transform(op: int, xf: int, a: np.ndarray, init):
+    a = np.ascontiguousarray(a)
+    iv = np.array([init], dtype=a.dtype)
+    out = np.zeros(1, a.dtype)
+    _ok(lib().lcor_reduce_transform(op, xf, _code(a), _p(a), a.size, _p(iv), _p(out)), "reduce_transform")
     return out[0]
 
 

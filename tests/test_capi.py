@@ -64,6 +64,12 @@ def test_temp_bytes_queries(L):
     assert rc == 0 and b == 2048 * 4
     rc, b = _q(L.lcpp_reduce_temp_bytes, 5, 1 << 28)
     assert rc == 0 and b == 2048 * 8
+    # arg reduce: one (value, index) partial per workgroup
+    rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 2, 1 << 28)
+    assert rc == 0 and b == 2048 * 8
+    rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 5, 1 << 28)
+    assert rc == 0 and b == 2048 * 16
+    assert _q(L.lcpp_reduce_arg_temp_bytes, 0, 100) == (0, 0)
     # scan: one packed 64-bit word per 16384-element tile (two per 8192-element
     # tile for 64-bit types)
     rc, b = _q(L.lcpp_scan_temp_bytes, 1, 1 << 28)
@@ -87,6 +93,12 @@ def test_unsupported_dtype_and_null_args(L):
     # argument errors are detected before any HIP call (no GPU here)
     assert L.lcpp_reduce_sum(9, None, 0, None, None, 10, None) == -3
     assert L.lcpp_reduce_sum(0, None, 0, None, None, 10, None) == -1
+    assert L.lcpp_reduce_argmin(0, None, 0, None, None, None, 10, None) == -1
+    assert L.lcpp_reduce_argmax(9, None, 0, None, None, None, 10, None) == -3
+    one = ctypes.c_int(1)
+    assert L.lcpp_reduce_transform(0, 0, 0, None, 0, None, None, 10, None, None) == -1  # init missing
+    assert L.lcpp_reduce_transform(0, 7, 0, None, 0, None, None, 10, ctypes.byref(one), None) == -1  # bad op
+    assert L.lcpp_reduce_transform(0, 0, 9, None, 0, None, None, 10, ctypes.byref(one), None) == -1  # bad transform
     assert L.lcpp_scan_exclusive_sum(0, None, 0, None, None, 10, None) == -1
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 10, None) == -1
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 1 << 30, None) == -1  # n >= 2^30

@@ -1,4 +1,5 @@
-"""DeviceReduce::Sum/Min/Max on the GPU through the C ABI, against the oracle
+"""DeviceReduce::Sum/Min/Max/ArgMin/ArgMax/TransformReduce on the GPU through
+the C ABI, against the oracle
 (bit-exact for integers; float sums within |err| <= 1e-5 * sum|x| of a
 float64 reduction)."""
 import numpy as np
@@ -119,3 +120,104 @@ def test_full_size_float32(gpu):
     got = run("Sum", d, n, np.float32)
     s, ab = o.reduce_f64(g.to_host(d))
     assert abs(float(got) - s) <= RTOL_SUM * ab
+
+
+# ------------------------------------------------------------------ ArgMin / ArgMax
+def run_arg(is_max, d_in, n, dtype):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce
+
+    out = g.empty(1, dtype)
+    idx = g.empty(1, np.uint32)
+    tmp = g.temp(DeviceReduce.GetArgTempStorageBytes(np.dtype(dtype).name, n))
+    (DeviceReduce().ArgMax if is_max else DeviceReduce().ArgMin)(tmp, d_in, out, idx, n)
+    return g.to_host(out)[0], int(g.to_host(idx)[0])
+
+
+def test_arg_kat_shuffled(gpu):
+    # device_reduce_test.cpp:169-225: shuffled 0..4095, std::min_element / max_element
+    import gpu_util as g
+
+    a = golden("reduce_shuffled_4096_i32.bin", np.int32)
+    d = g.to_dev(a)
+    assert run_arg(False, d, a.size, np.int32) == (0, int(np.nonzero(a == 0)[0][0]))
+    assert run_arg(True, d, a.size, np.int32) == (4095, int(np.nonzero(a == 4095)[0][0]))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 63, 4097, 32768, 1_000_003])
+def test_arg_vs_oracle_with_ties(gpu, dtype, n):
+    import gpu_util as g
+
+    rng = np.random.default_rng(n)
+    a = rng.integers(0, 97, size=n).astype(dtype)  # many ties: the index rule decides
+    log(f"argmin/argmax {np.dtype(dtype).name} n={n}")
+    d = g.to_dev(a)
+    for is_max in (False, True):
+        v, i = run_arg(is_max, d, n, dtype)
+        ev, ei = o.reduce_arg(is_max, a)
+        assert (v, i) == (ev, ei)
+
+
+def test_arg_empty(gpu):
+    import gpu_util as g
+
+    d = g.empty(4, np.int32)
+    assert run_arg(False, d, 0, np.int32) == (np.iinfo(np.int32).max, 0xFFFFFFFF)
+    f = g.empty(4, np.float32)
+    assert run_arg(True, f, 0, np.float32) == (np.finfo(np.float32).min, 0)
+
+
+def test_arg_full_size_int32(gpu):
+    # 2^28 values in [-1000, 1000]: ArgMin = first -1000, ArgMax = last 1000
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    log("argmin/argmax int32 full 2^28")
+    d = datagen.reduce_i32(n)
+    h = g.to_host(d)
+    assert run_arg(False, d, n, np.int32) == (-1000, int(np.argmin(h)))
+    assert run_arg(True, d, n, np.int32) == (1000, n - 1 - int(np.argmax(h[::-1])))
+
+
+# ------------------------------------------------------------------ TransformReduce
+def run_transform(op, xf, d_in, n, dtype, init):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce
+
+    out = g.empty(1, dtype)
+    tmp = g.temp(DeviceReduce.GetTempStorageBytes(np.dtype(dtype).name, n))
+    DeviceReduce().TransformReduce(tmp, d_in, out, n, op, xf, init)
+    return g.to_host(out)[0]
+
+
+OPS = {"sum": o.OP_SUM, "min": o.OP_MIN, "max": o.OP_MAX}
+XFS = {"identity": o.XF_IDENTITY, "negate": o.XF_NEGATE, "abs": o.XF_ABS, "square": o.XF_SQUARE}
+
+
+def test_transform_kat_max_of_squares(gpu):
+    # device_reduce_test.cpp:92-117
+    import gpu_util as g
+
+    a = golden("reduce_shuffled_4096_i32.bin", np.int32)
+    assert run_transform("max", "square", g.to_dev(a), a.size, np.int32, 0) == 4095 * 4095
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("op", list(OPS))
+@pytest.mark.parametrize("xf", list(XFS))
+def test_transform_vs_oracle(gpu, dtype, op, xf):
+    import gpu_util as g
+
+    n = 300_007
+    a = g.random_array(dtype, n, seed=17)
+    d = g.to_dev(a)
+    init = np.array([3], dtype=dtype)[0]
+    got = run_transform(op, xf, d, n, dtype, init)
+    if np.dtype(dtype).kind == "f" and op == "sum":
+        t = {"identity": a, "negate": -a, "abs": np.abs(a), "square": a * a}[xf].astype(np.float64)
+        s, ab = float(t.sum()) + float(init), float(np.abs(t).sum()) + abs(float(init))
+        assert abs(float(got) - s) <= RTOL_SUM * ab
+    else:
+        assert got == o.reduce_transform(OPS[op], XFS[xf], a, init)

@@ -96,6 +96,65 @@ def test_reduce_f64_against_fsum():
     assert ab == pytest.approx(float(np.abs(a.astype(np.float64)).sum()), rel=1e-12)
 
 
+def last_argmax(a: np.ndarray) -> int:
+    """Index of the last maximum (ArgMaxOp breaks ties to the larger index)."""
+    return a.size - 1 - int(np.argmax(a[::-1]))
+
+
+@pytest.mark.parametrize("dt", SORT_DTYPES)
+def test_reduce_arg_vs_numpy(dt):
+    rng = np.random.default_rng(21)
+    n = 60_007
+    if np.issubdtype(dt, np.floating):
+        a = rng.integers(-50, 50, size=n).astype(dt)  # many ties
+    else:
+        info = np.iinfo(dt)
+        a = rng.integers(max(info.min, -50), 50, size=n, endpoint=True).astype(dt)
+    v, i = o.reduce_arg(False, a)
+    assert i == int(np.argmin(a)) and v == a.min()  # first occurrence
+    v, i = o.reduce_arg(True, a)
+    assert i == last_argmax(a) and v == a.max()  # last occurrence
+    assert last_argmax(np.array([1, 3, 2, 3], dt)) == 3
+
+
+def test_reduce_arg_kat_shuffled():
+    # device_reduce_test.cpp:169-225: shuffled 0..4095, std::min/max_element
+    a = golden("reduce_shuffled_4096_i32.bin", np.int32)
+    assert o.reduce_arg(False, a) == (0, int(np.nonzero(a == 0)[0][0]))
+    assert o.reduce_arg(True, a) == (4095, int(np.nonzero(a == 4095)[0][0]))
+
+
+def test_reduce_arg_empty():
+    assert o.reduce_arg(False, np.zeros(0, np.int32)) == (np.iinfo(np.int32).max, 0xFFFFFFFF)
+    assert o.reduce_arg(True, np.zeros(0, np.float32)) == (np.finfo(np.float32).min, 0)
+
+
+NP_XF = {o.XF_IDENTITY: lambda a: a, o.XF_NEGATE: np.negative, o.XF_ABS: np.abs,
+         o.XF_SQUARE: lambda a: np.multiply(a, a)}
+NP_OP = {o.OP_SUM: np.sum, o.OP_MIN: np.min, o.OP_MAX: np.max}
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint32, np.int64, np.uint64])
+@pytest.mark.parametrize("xf", [o.XF_IDENTITY, o.XF_NEGATE, o.XF_ABS, o.XF_SQUARE])
+@pytest.mark.parametrize("op", [o.OP_SUM, o.OP_MIN, o.OP_MAX])
+def test_reduce_transform_integers_vs_numpy(dt, xf, op):
+    rng = np.random.default_rng(xf * 3 + op)
+    info = np.iinfo(dt)
+    a = rng.integers(info.min, info.max, size=20_011, dtype=dt, endpoint=True)
+    with np.errstate(over="ignore"):
+        t = NP_XF[xf](a).astype(dt)  # element-type wraparound
+        red = NP_OP[op](t, dtype=dt) if op == o.OP_SUM else NP_OP[op](t)
+        init = dt(7)
+        exp = NP_OP[op](np.array([init, red], dtype=dt), dtype=dt) if op == o.OP_SUM else NP_OP[op]([init, red])
+    assert o.reduce_transform(op, xf, a, init) == exp
+
+
+def test_reduce_transform_kat_max_of_squares():
+    # device_reduce_test.cpp:92-117: max over shuffled 0..4095 of x*x, init 0 -> 4095^2
+    a = golden("reduce_shuffled_4096_i32.bin", np.int32)
+    assert o.reduce_transform(o.OP_MAX, o.XF_SQUARE, a, 0) == 4095 * 4095
+
+
 # ------------------------------------------------------------------ scan
 def test_scan_kat_ones():
     # device_scan_test.cpp:67-108: ones -> exclusive i, inclusive i+1
