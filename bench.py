@@ -42,6 +42,11 @@ def measured_traffic():
     return None
 
 
+def progress(msg):
+    """One line per finished stage on stderr (the JSON line stays alone on stdout)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,6 +133,7 @@ def main():
 
     ms = timed(sort_call, args.steps, args.warmup)
     gkeys = n / (ms * 1e-3) / 1e9
+    progress(f"SortKeys u32 2^28: {ms:.4f} ms/step, {gkeys:.2f} Gkeys/s")
     pass_ms, pass_launches, rec = kernel_ms(sort_call, max(2, args.steps // 4), "rs_onesweep")
     pass_bytes = 8 * n  # read 4N + write 4N per onesweep pass (algorithmic)
     achieved = pass_bytes / (pass_ms * 1e-3) / 1e9
@@ -184,6 +190,7 @@ def main():
             if items is not None:
                 entry["Gitems/s"] = round(items / (t * 1e-3) / 1e9, 3)
             sec.append(entry)
+            progress(f"{name}: {entry['ms']} ms")
 
         def want(name):
             return args.only is None or args.only == name
@@ -269,6 +276,7 @@ def main():
     # ------------------------------------------------------------ CPU baseline (oracle onesweep port)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
+        progress(f"cpu baseline: {result['cpu_baseline']['value']} Gkeys/s")
 
     print(json.dumps(result), flush=True)
 
