@@ -91,7 +91,7 @@ constexpr lcpp_reduce_op reduce_op_of()
     if constexpr (std::is_same_v<Op, SumOp>) return LCPP_OP_SUM;
     else if constexpr (std::is_same_v<Op, MinOp>) return LCPP_OP_MIN;
     else if constexpr (std::is_same_v<Op, MaxOp>) return LCPP_OP_MAX;
-    else static_assert(sizeof(Op) == 0, "TransformReduce: reduce_op must be SumOp, MinOp or MaxOp");
+    else static_assert(sizeof(Op) == 0, "reduce_op / scan_op must be SumOp, MinOp or MaxOp");
 }
 template <class Xf>
 constexpr lcpp_transform transform_of()
@@ -210,9 +210,30 @@ class DeviceReduce : public LuisaModule {
                                     num_item, &init, cmdlist.stream),
               "DeviceReduce::TransformReduce");
     }
+    /* device/device_reduce.h:110-125 */
+    template <class KeyType, class ValueType>
+    static size_t GetReduceByKeyTempStorageBytes(size_t num_elements)
+    {
+        size_t b = 0;
+        lcpp_reduce_by_key_temp_bytes(dtype_of<KeyType>(), dtype_of<ValueType>(), num_elements, &b);
+        return b;
+    }
+    /* device/device_reduce.h:277-318 (reduce_op: SumOp, MinOp or MaxOp) */
+    template <class KeyType, class ValueType, class ReduceOp>
+    void ReduceByKey(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                     BufferView<ValueType> d_values_in, BufferView<KeyType> d_unique_out,
+                     BufferView<ValueType> g_aggregates_out, BufferView<uint> g_num_runs_out, ReduceOp,
+                     size_t num_elements)
+    {
+        check(lcpp_reduce_by_key(dtype_of<KeyType>(), dtype_of<ValueType>(), reduce_op_of<ReduceOp>(),
+                                 temp_storage.data(), temp_storage.size_bytes(), d_keys_in.data(), d_values_in.data(),
+                                 d_unique_out.data(), g_aggregates_out.data(), g_num_runs_out.data(), num_elements,
+                                 cmdlist.stream),
+              "DeviceReduce::ReduceByKey");
+    }
 };
 
-/* device/device_scan.h:33-204 */
+/* device/device_scan.h:33-339 */
 template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
           size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
 class DeviceScan : public LuisaModule {
@@ -239,6 +260,58 @@ class DeviceScan : public LuisaModule {
         check(lcpp_scan_inclusive_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                       d_out.data(), num_items, cmdlist.stream),
               "DeviceScan::InclusiveSum");
+    }
+    /* device/device_scan.h:91-107 */
+    template <class KeyType, class ValueType>
+    static size_t GetScanByKeyTempStorageBytes(size_t num_items)
+    {
+        size_t b = 0;
+        lcpp_scan_by_key_temp_bytes(dtype_of<KeyType>(), dtype_of<ValueType>(), num_items, &b);
+        return b;
+    }
+    /* device/device_scan.h:206-254 (scan_op: SumOp, MinOp or MaxOp) */
+    template <class KeyType, class ValueType, class ScanOp>
+    void ExclusiveScanByKey(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, ScanOp,
+                            size_t num_items, ValueType initial_value)
+    {
+        check(lcpp_scan_exclusive_by_key(dtype_of<KeyType>(), dtype_of<ValueType>(), reduce_op_of<ScanOp>(),
+                                         temp_storage.data(), temp_storage.size_bytes(), d_keys_in.data(),
+                                         d_values_in.data(), d_values_out.data(), num_items, &initial_value,
+                                         cmdlist.stream),
+              "DeviceScan::ExclusiveScanByKey");
+    }
+    /* device/device_scan.h:256-303 (heads get scan_op(value, init); the reference gives init) */
+    template <class KeyType, class ValueType, class ScanOp>
+    void InclusiveScanByKey(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, ScanOp,
+                            size_t num_items, ValueType initial_value)
+    {
+        check(lcpp_scan_inclusive_by_key(dtype_of<KeyType>(), dtype_of<ValueType>(), reduce_op_of<ScanOp>(),
+                                         temp_storage.data(), temp_storage.size_bytes(), d_keys_in.data(),
+                                         d_values_in.data(), d_values_out.data(), num_items, &initial_value,
+                                         cmdlist.stream),
+              "DeviceScan::InclusiveScanByKey");
+    }
+    /* device/device_scan.h:306-322 */
+    template <class T>
+    void ExclusiveSumByKey(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_keys_in,
+                           BufferView<T> d_values_in, BufferView<T> d_values_out, size_t num_items)
+    {
+        check(lcpp_scan_exclusive_sum_by_key(dtype_of<T>(), dtype_of<T>(), temp_storage.data(),
+                                             temp_storage.size_bytes(), d_keys_in.data(), d_values_in.data(),
+                                             d_values_out.data(), num_items, cmdlist.stream),
+              "DeviceScan::ExclusiveSumByKey");
+    }
+    /* device/device_scan.h:324-339 */
+    template <class T>
+    void InclusiveSumByKey(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_keys_in,
+                           BufferView<T> d_values_in, BufferView<T> d_values_out, size_t num_items)
+    {
+        check(lcpp_scan_inclusive_sum_by_key(dtype_of<T>(), dtype_of<T>(), temp_storage.data(),
+                                             temp_storage.size_bytes(), d_keys_in.data(), d_values_in.data(),
+                                             d_values_out.data(), num_items, cmdlist.stream),
+              "DeviceScan::InclusiveSumByKey");
     }
 };
 

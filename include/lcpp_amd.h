@@ -122,6 +122,47 @@ int lcpp_scan_inclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const v
                             void *out, uint64_t n, void *stream);
 
 /* ---------------------------------------------------------------------
+ * ScanByKey / ReduceByKey — device/device_scan.h, device/device_reduce.h
+ * Segments are maximal runs of equal consecutive keys: element i is a
+ * segment head when i == 0 or keys[i] != keys[i-1], compared in the key
+ * type (floating keys: -0.0 == +0.0, NaN != NaN).  Keys and values: any
+ * lcpp_dtype.  The reference takes arbitrary device functors; the C ABI
+ * carries lcpp_reduce_op.  *init is a host value of the value type (NULL
+ * means 0).
+ * ------------------------------------------------------------------- */
+/* replaces DeviceScan::GetScanByKeyTempStorageBytes<K,V>(num_items), device_scan.h:91-107 */
+int lcpp_scan_by_key_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint64_t n, size_t *bytes);
+/* replaces DeviceScan::ExclusiveScanByKey(cmdlist, temp, d_keys_in, d_values_in, d_values_out,
+ * scan_op, num_items, initial_value), device_scan.h:206-254:
+ * out[i] = init at a head, else op(fold(vals_in[head..i)), init) */
+int lcpp_scan_exclusive_by_key(lcpp_dtype k, lcpp_dtype v, lcpp_reduce_op op, void *temp,
+                               size_t temp_bytes, const void *keys_in, const void *vals_in,
+                               void *vals_out, uint64_t n, const void *init, void *stream);
+/* replaces DeviceScan::InclusiveScanByKey, device_scan.h:256-303:
+ * out[i] = op(fold(vals_in[head..i]), init).  (The reference overwrites every head with init,
+ * scan_by_key.h:113-128; heads here get op(vals_in[head], init).) */
+int lcpp_scan_inclusive_by_key(lcpp_dtype k, lcpp_dtype v, lcpp_reduce_op op, void *temp,
+                               size_t temp_bytes, const void *keys_in, const void *vals_in,
+                               void *vals_out, uint64_t n, const void *init, void *stream);
+/* replaces DeviceScan::ExclusiveSumByKey, device_scan.h:306-322 (sum, init 0) */
+int lcpp_scan_exclusive_sum_by_key(lcpp_dtype k, lcpp_dtype v, void *temp, size_t temp_bytes,
+                                   const void *keys_in, const void *vals_in, void *vals_out,
+                                   uint64_t n, void *stream);
+/* replaces DeviceScan::InclusiveSumByKey, device_scan.h:324-339 (sum, init 0) */
+int lcpp_scan_inclusive_sum_by_key(lcpp_dtype k, lcpp_dtype v, void *temp, size_t temp_bytes,
+                                   const void *keys_in, const void *vals_in, void *vals_out,
+                                   uint64_t n, void *stream);
+/* replaces DeviceReduce::GetReduceByKeyTempStorageBytes<K,V>(num_elements), device_reduce.h:110-125 */
+int lcpp_reduce_by_key_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint64_t n, size_t *bytes);
+/* replaces DeviceReduce::ReduceByKey(cmdlist, temp, d_keys_in, d_values_in, d_unique_out,
+ * g_aggregates_out, g_num_runs_out, reduce_op, num_elements), device_reduce.h:277-318:
+ * run r: unique_out[r] = its key, aggregates_out[r] = op-fold of its values;
+ * *num_runs_out (device memory) = number of runs.  Outputs hold up to n entries.  n < 2^32. */
+int lcpp_reduce_by_key(lcpp_dtype k, lcpp_dtype v, lcpp_reduce_op op, void *temp, size_t temp_bytes,
+                       const void *keys_in, const void *vals_in, void *unique_out,
+                       void *aggregates_out, uint32_t *num_runs_out, uint64_t n, void *stream);
+
+/* ---------------------------------------------------------------------
  * DeviceRadixSort (onesweep, all key bits) — device/device_radix_sort.h
  * Keys: any lcpp_dtype (signed and floating keys are bit-twiddled as in
  * common/util_type.h:98-175; -0.0 and +0.0 compare equal).  Values: any

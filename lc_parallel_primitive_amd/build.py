@@ -18,7 +18,8 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "liblcpp_amd.so")
 DATAGEN_LIB = os.path.join(PKG, "liblcpp_datagen.so")
 
-LIB_SOURCES = ["runtime.hip", "reduce.hip", "scan.hip", "radix_sort.hip", "segment_reduce.hip"]
+LIB_SOURCES = ["runtime.hip", "reduce.hip", "scan.hip", "radix_sort.hip", "segment_reduce.hip",
+               "scan_by_key.hip", "reduce_by_key.hip"]
 DATAGEN_SOURCES = ["datagen.hip"]
 
 ARCH = os.environ.get("LCPP_OFFLOAD_ARCH", "gfx950")

@@ -1,0 +1,156 @@
+// lookback.hpp — single-pass decoupled look-back over packed 64-bit words.
+//
+// Reference: device/details/single_pass_scan_operator.h:25-251
+// (ScanTileStatus, ScanTileStateViewer, TilePrefixCallbackOp).
+//
+// Each tile owns self-validating words written with agent-scope relaxed
+// stores (the 8 XCD L2s of an MI355X are not coherent with each other):
+//   4-byte payload: one word  {payload:32 | status:32}
+//   8-byte payload: two words {lo:32 | status:32}, {hi:32 | status:32}
+// A reader accepts a tile only when the statuses of its words agree.  Each
+// status value is written at most once per word, so agreeing statuses come
+// from one publish and no fence is needed.  The reference keeps status and
+// values in separate arrays with no ordering between them
+// (single_pass_scan_operator.h:81-93); release/acquire pairs instead cost
+// an L2 write-back/invalidate per publish on this part.
+//
+// The prefix wait is executed by all 64 lanes of one wave: lane l polls
+// predecessor top - l, all loads issued before any wait, and the wave stops
+// at the nearest INCLUSIVE tile, waiting only for closer predecessors.
+#pragma once
+
+#include "common.hpp"
+
+namespace lcpp {
+
+constexpr uint32_t kStInvalid = 0, kStPartial = 1, kStInclusive = 2;
+
+template <class T>
+constexpr int lb_words()
+{
+    return sizeof(T) == 4 ? 1 : 2;
+}
+
+template <class T>
+__device__ __forceinline__ uint64_t lb_bits(T v)
+{
+    if constexpr (sizeof(T) == 4) return __builtin_bit_cast(uint32_t, v);
+    else return __builtin_bit_cast(uint64_t, v);
+}
+template <class T>
+__device__ __forceinline__ T lb_from_bits(uint64_t b)
+{
+    if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, (uint32_t)b);
+    else return __builtin_bit_cast(T, b);
+}
+
+template <class T>
+__device__ __forceinline__ void lb_publish(uint64_t *words, uint32_t tile, T v, uint32_t status)
+{
+    const uint64_t b = lb_bits(v);
+    if constexpr (sizeof(T) == 4) {
+        st_relaxed(&words[tile], (b << 32) | status);
+    } else {
+        st_relaxed(&words[2 * (uint64_t)tile], (uint64_t)((b << 32) | status));
+        st_relaxed(&words[2 * (uint64_t)tile + 1], (uint64_t)((b & 0xFFFFFFFF00000000ull) | status));
+    }
+}
+
+// Exclusive prefix of `tile` (tile > 0): the op-fold of the aggregates of
+// the tiles after the nearest INCLUSIVE predecessor, folded onto that
+// predecessor's inclusive value.  Every lane returns it.  `op` must be
+// commutative (sum, min, max): a window is reduced as a tree.
+template <class T, class Op>
+__device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T identity)
+{
+    const uint32_t lane = lane_id();
+    T excl = identity;
+    int64_t top = (int64_t)tile - 1;
+    uint32_t spins = 0;
+    for (;;) {
+        // Lane l polls predecessor top - l.  The load is unconditional (an
+        // index below 0 reads word 0 and is then treated as INCLUSIVE
+        // identity), so the compiler issues it without a branch around it.
+        const int64_t j = top - (int64_t)lane;
+        const uint64_t jj = j < 0 ? 0 : (uint64_t)j;
+        uint32_t s;
+        T v;
+        if constexpr (sizeof(T) == 4) {
+            const uint64_t w = ld_relaxed(&words[jj]);
+            s = (uint32_t)w;
+            v = lb_from_bits<T>(w >> 32);
+        } else {
+            const uint64_t lo = ld_relaxed(&words[2 * jj]);
+            const uint64_t hi = ld_relaxed(&words[2 * jj + 1]);
+            s = (uint32_t)lo == (uint32_t)hi ? (uint32_t)lo : kStInvalid;
+            v = lb_from_bits<T>((hi & 0xFFFFFFFF00000000ull) | (lo >> 32));
+        }
+        if (j < 0) {
+            s = kStInclusive;
+            v = identity;
+        }
+        const uint64_t incl = ballot(s == kStInclusive);
+        const uint32_t stop = incl ? (uint32_t)__builtin_ctzll(incl) : (uint32_t)(kWave - 1);
+        const bool in_range = lane <= stop;
+        if (ballot(in_range && s == kStInvalid) != 0 && ++spins < kSpinLimit) {
+            __builtin_amdgcn_s_sleep(1);
+            continue;  // re-poll the same window
+        }
+        excl = op(excl, wave_allreduce(in_range ? v : identity, op));
+        if (incl) break;
+        top -= kWave;
+    }
+    return excl;
+}
+
+// Plain scan tile: publish PARTIAL(agg), wait for the prefix, publish
+// INCLUSIVE(prefix op agg).  Returns the exclusive prefix (identity for
+// tile 0) in every lane.
+template <class T, class Op>
+__device__ __forceinline__ T lb_scan_tile(uint64_t *words, uint32_t tile, T agg, Op op, T identity)
+{
+    const uint32_t lane = lane_id();
+    if (tile == 0) {
+        if (lane == 0) lb_publish(words, 0, agg, kStInclusive);
+        return identity;
+    }
+    if (lane == 0) lb_publish(words, tile, agg, kStPartial);
+    const T excl = lb_wait_prefix(words, tile, op, identity);
+    if (lane == 0) lb_publish(words, tile, op(excl, agg), kStInclusive);
+    return excl;
+}
+
+// Segmented (by-key) scan tile.  A tile that contains a segment head knows
+// its inclusive value at once (the fold since its last head) and publishes
+// INCLUSIVE(agg) before it waits; it waits only if its first element is not
+// a head (`need_prefix`).  A tile without a head is a plain scan tile.
+template <class T, class Op>
+__device__ __forceinline__ T lb_segmented_tile(uint64_t *words, uint32_t tile, T agg, bool has_head,
+                                              bool need_prefix, Op op, T identity)
+{
+    if (!has_head) return lb_scan_tile(words, tile, agg, op, identity);
+    if (lane_id() == 0) lb_publish(words, tile, agg, kStInclusive);
+    if (tile == 0 || !need_prefix) return identity;
+    return lb_wait_prefix(words, tile, op, identity);
+}
+
+namespace {
+__global__ __launch_bounds__(256) void lb_init_kernel(uint64_t *words, uint64_t count)
+{
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) words[i] = 0;
+}
+
+// Zero `count` look-back words on stream s (grid-stride fill kernel; a
+// kernel rather than hipMemsetAsync so the call can be graph-captured).
+int lb_init(uint64_t *words, uint64_t count, hipStream_t s, const char *name)
+{
+    if (!count) return LCPP_OK;
+    const uint64_t g = ceil_div(count, 256);
+    const uint32_t grid = (uint32_t)(g < 1024 ? g : 1024);
+    LCPP_LAUNCH(name, s, lb_init_kernel<<<grid, 256, 0, s>>>(words, count));
+    return hipGetLastError() == hipSuccess ? LCPP_OK : LCPP_ERR_HIP;
+}
+}  // namespace
+
+}  // namespace lcpp

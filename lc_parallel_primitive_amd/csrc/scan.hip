@@ -18,32 +18,25 @@
 //    workgroups per CU (~100 VGPRs).
 //  * Loads and stores are raw-buffer instructions on a resource that ends at
 //    the tile's last valid byte: a ragged last tile and unaligned pointers take
-//    the element-wise path with no per-element bounds logic.
+//    the element-wise path with no per-element bounds logic.  That path keeps
+//    the whole offset in the VGPR operand, which the range check covers (the
+//    scalar offset operand is used only by full tiles).
 //  * Tile id = blockIdx.x, as the reference (scan.h:76).  Workgroups are
 //    dispatched in id order, so every predecessor of a waiting tile is
 //    already resident or finished.  (A dynamic ticket costs one same-address
 //    atomic per tile, ~11 ns each, which serialises the whole grid.)
-//  * Look-back state per tile is self-validating packed words written with
-//    agent-scope relaxed stores: 32-bit types use one 64-bit word
-//    {value:32 | status:32}; 64-bit types use two words {value_lo | status}
-//    and {value_hi | status}, read as valid only when both statuses agree
-//    (each status is written once per word, so agreeing statuses come from
-//    one publish).  The reference keeps status and value in separate arrays
-//    with no ordering between them (single_pass_scan_operator.h:81-93);
-//    release/acquire pairs instead cost an L2 write-back/invalidate per
-//    publish on this part (7.8 ms for 2^27 x 64-bit).
-//  * Wave 0 issues all 64 predecessor polls at once (branch-free, so they
-//    are in flight together), stops at the nearest INCLUSIVE and only waits
-//    for predecessors closer than it.
-#include "common.hpp"
+//  * Look-back (lookback.hpp): one self-validating packed word per tile
+//    (two for 64-bit types) written with agent-scope relaxed stores
+//    (release/acquire pairs cost an L2 write-back/invalidate per publish on
+//    this part: 7.8 ms for 2^27 x 64-bit); wave 0 polls 64 predecessors at
+//    once and stops at the nearest INCLUSIVE.
+#include "lookback.hpp"
 
 namespace lcpp {
 namespace {
 
 constexpr int kScanBlock = 256;
 constexpr int kScanVecs = 16;
-constexpr uint32_t kStInvalid = 0, kStPartial = 1, kStInclusive = 2;
-
 template <class T>
 constexpr uint32_t scan_tile()
 {
@@ -61,89 +54,6 @@ template <class T>
 uint64_t scan_temp_bytes(uint64_t n)
 {
     return align_up(scan_tiles<T>(n) * (sizeof(T) == 4 ? 8 : 16), 256);
-}
-
-template <class T>
-__device__ __forceinline__ uint64_t to_bits(T v)
-{
-    if constexpr (sizeof(T) == 4) return __builtin_bit_cast(uint32_t, v);
-    else return __builtin_bit_cast(uint64_t, v);
-}
-template <class T>
-__device__ __forceinline__ T from_bits(uint64_t b)
-{
-    if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, (uint32_t)b);
-    else return __builtin_bit_cast(T, b);
-}
-
-template <class T>
-__device__ __forceinline__ void publish(uint64_t *words, uint32_t tile, T v, uint32_t status)
-{
-    const uint64_t b = to_bits(v);
-    if constexpr (sizeof(T) == 4) {
-        st_relaxed(&words[tile], (b << 32) | status);
-    } else {
-        st_relaxed(&words[2 * (uint64_t)tile], (uint64_t)((b << 32) | status));
-        st_relaxed(&words[2 * (uint64_t)tile + 1], (uint64_t)((b & 0xFFFFFFFF00000000ull) | status));
-    }
-}
-
-// Decoupled look-back, executed by all 64 lanes of one wave.  Returns the
-// exclusive prefix of `tile` in every lane and publishes INCLUSIVE.
-template <class T>
-__device__ T lookback(uint64_t *words, uint32_t tile, T agg)
-{
-    SumOp op;
-    const uint32_t lane = lane_id();
-    if (tile == 0) {
-        if (lane == 0) publish(words, 0, agg, kStInclusive);
-        return T(0);
-    }
-    if (lane == 0) publish(words, tile, agg, kStPartial);
-    T excl = T(0);
-    int64_t top = (int64_t)tile - 1;
-    uint32_t spins = 0;
-    for (;;) {
-        // Lane l polls predecessor top - l.  The load is unconditional (an
-        // index below 0 reads word 0 and is then treated as INCLUSIVE 0), so
-        // the compiler issues it without a branch around it.
-        const int64_t j = top - (int64_t)lane;
-        const uint64_t jj = j < 0 ? 0 : (uint64_t)j;
-        uint32_t s;
-        T v;
-        if constexpr (sizeof(T) == 4) {
-            const uint64_t w = ld_relaxed(&words[jj]);
-            s = (uint32_t)w;
-            v = from_bits<T>(w >> 32);
-        } else {
-            const uint64_t lo = ld_relaxed(&words[2 * jj]);
-            const uint64_t hi = ld_relaxed(&words[2 * jj + 1]);
-            s = (uint32_t)lo == (uint32_t)hi ? (uint32_t)lo : kStInvalid;
-            v = from_bits<T>((hi & 0xFFFFFFFF00000000ull) | (lo >> 32));
-        }
-        if (j < 0) {
-            s = kStInclusive;
-            v = T(0);
-        }
-        const uint64_t incl = ballot(s == kStInclusive);
-        const uint32_t stop = incl ? (uint32_t)__builtin_ctzll(incl) : (uint32_t)(kWave - 1);
-        const bool in_range = lane <= stop;
-        if (ballot(in_range && s == kStInvalid) != 0 && ++spins < kSpinLimit) {
-            __builtin_amdgcn_s_sleep(1);
-            continue;  // re-poll the same window
-        }
-        excl = op(excl, wave_allreduce(in_range ? v : T(0), op));
-        if (incl) break;
-        top -= kWave;
-    }
-    if (lane == 0) publish(words, tile, op(excl, agg), kStInclusive);
-    return excl;
-}
-
-__global__ __launch_bounds__(256) void scan_init_kernel(uint64_t *words, uint64_t count)
-{
-    const uint64_t stride = (uint64_t)gridDim.x * 256;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) words[i] = 0;
 }
 
 template <class T, bool INCLUSIVE>
@@ -178,7 +88,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ 
 #pragma unroll
         for (int k = 0; k < K; ++k)
 #pragma unroll
-            for (int j = 0; j < V; ++j) x[k][j] = buf_ld_elem<T>(rin, tid * 16 + j * sizeof(T), k * CHUNK);
+            for (int j = 0; j < V; ++j) x[k][j] = buf_ld_elem<T>(rin, k * CHUNK + tid * 16 + j * sizeof(T), 0);
     }
 
     // Per chunk: thread scan in place, wave scan of the thread totals, wave
@@ -214,7 +124,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ 
         for (int k = 0; k < K; ++k)
 #pragma unroll
             for (int w = 0; w < W; ++w) agg = op(agg, s_wtot[k][w]);
-        const T ex = lookback(words, tile, agg);
+        const T ex = lb_scan_tile(words, tile, agg, op, T(0));
         if (lane == 0) s_prefix = ex;
     }
     __syncthreads();
@@ -242,7 +152,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ 
 #pragma unroll
         for (int k = 0; k < K; ++k)
 #pragma unroll
-            for (int j = 0; j < V; ++j) buf_st_elem<T>(rout, tid * 16 + j * sizeof(T), k * CHUNK, x[k][j]);
+            for (int j = 0; j < V; ++j) buf_st_elem<T>(rout, k * CHUNK + tid * 16 + j * sizeof(T), 0, x[k][j]);
     }
 }
 
@@ -260,9 +170,7 @@ int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, 
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
     uint64_t *words = static_cast<uint64_t *>(temp);
     const uint64_t nwords = tiles * (sizeof(T) == 4 ? 1 : 2);
-    const uint32_t init_grid = (uint32_t)(ceil_div(nwords, 256) < 1024 ? ceil_div(nwords, 256) : 1024);
-    LCPP_LAUNCH("scan_init", s, scan_init_kernel<<<init_grid, 256, 0, s>>>(words, nwords));
-    LCPP_CHECK_LAUNCH();
+    if (lb_init(words, nwords, s, "scan_init") != LCPP_OK) return LCPP_ERR_HIP;
     const int vec_ok = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     if (inclusive)
         LCPP_LAUNCH("scan_inclusive", s,

@@ -50,6 +50,17 @@ def _same_dtype(a, b, what: str):
         raise TypeError(f"{what}: dtype mismatch {a.dtype} vs {b.dtype}")
 
 
+_NP_DTYPES = ["int32", "uint32", "float32", "int64", "uint64", "float64"]
+
+
+def _host_value(code: int, value):
+    """A one-element numpy array of lcpp_dtype `code` holding `value` (kept
+    alive by the caller for the duration of the call)."""
+    import numpy as np
+
+    return np.array([value], dtype=_NP_DTYPES[code])
+
+
 def _query(fn, *args) -> int:
     out = ctypes.c_size_t()
     check(fn(*args, ctypes.byref(out)), fn.__name__)
@@ -57,7 +68,7 @@ def _query(fn, *args) -> int:
 
 
 class DeviceReduce:
-    """device/device_reduce.h:37-348 (Sum / Min / Max / ArgMin / ArgMax / TransformReduce)."""
+    """device/device_reduce.h:37-348 (Sum / Min / Max / ArgMin / ArgMax / ReduceByKey / TransformReduce)."""
 
     def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
         # geometry is fixed per dtype inside the library (tuned for gfx950);
@@ -128,9 +139,35 @@ class DeviceReduce:
                                           ctypes.c_void_p(iv.ctypes.data), _stream(stream)),
               "lcpp_reduce_transform")
 
+    @staticmethod
+    def GetReduceByKeyTempStorageBytes(key_dtype, value_dtype, num_elements: int) -> int:
+        """device_reduce.h:110-125"""
+        return _query(lib().lcpp_reduce_by_key_temp_bytes, dtype_code(key_dtype), dtype_code(value_dtype),
+                      num_elements)
+
+    def ReduceByKey(self, temp_storage, d_keys_in, d_values_in, d_unique_out, g_aggregates_out, g_num_runs_out,
+                    reduce_op: str, num_elements: int, stream=None):
+        """device_reduce.h:277-318: one (key, op-fold of values) per run of equal consecutive keys;
+        g_num_runs_out[0] (a device uint32) = number of runs.  reduce_op: "sum" | "min" | "max"."""
+        for t, nm in ((d_keys_in, "d_keys_in"), (d_values_in, "d_values_in"), (d_unique_out, "d_unique_out"),
+                      (g_aggregates_out, "g_aggregates_out")):
+            _need(t, num_elements, nm)
+        _need(g_num_runs_out, 1, "g_num_runs_out")
+        _same_dtype(d_keys_in, d_unique_out, "ReduceByKey keys")
+        _same_dtype(d_values_in, g_aggregates_out, "ReduceByKey values")
+        if g_num_runs_out.element_size() != 4:
+            raise TypeError("ReduceByKey: g_num_runs_out must hold a 32-bit count")
+        if reduce_op not in LCPP_OPS:
+            raise ValueError(f"ReduceByKey: unsupported reduce_op {reduce_op!r}")
+        check(lib().lcpp_reduce_by_key(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype), LCPP_OPS[reduce_op],
+                                       _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_keys_in), _ptr(d_values_in),
+                                       _ptr(d_unique_out), _ptr(g_aggregates_out), _ptr(g_num_runs_out), num_elements,
+                                       _stream(stream)),
+              "lcpp_reduce_by_key")
+
 
 class DeviceScan:
-    """device/device_scan.h:33-204 (ExclusiveSum / InclusiveSum)."""
+    """device/device_scan.h:33-339 (ExclusiveSum / InclusiveSum / *ScanByKey / *SumByKey)."""
 
     def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
         self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
@@ -154,6 +191,45 @@ class DeviceScan:
 
     def InclusiveSum(self, temp_storage, d_in, d_out, num_items: int, stream=None):
         self._run(lib().lcpp_scan_inclusive_sum, temp_storage, d_in, d_out, num_items, stream)
+
+    @staticmethod
+    def GetScanByKeyTempStorageBytes(key_dtype, value_dtype, num_items: int) -> int:
+        """device_scan.h:91-107"""
+        return _query(lib().lcpp_scan_by_key_temp_bytes, dtype_code(key_dtype), dtype_code(value_dtype), num_items)
+
+    def _by_key(self, fn, name, temp, d_keys_in, d_values_in, d_values_out, num_items, op, init, stream):
+        _need(d_keys_in, num_items, "d_keys_in")
+        _need(d_values_in, num_items, "d_values_in")
+        _need(d_values_out, num_items, "d_values_out")
+        _same_dtype(d_values_in, d_values_out, name)
+        if op not in LCPP_OPS:
+            raise ValueError(f"{name}: unsupported scan_op {op!r}")
+        vcode = dtype_code(d_values_in.dtype)
+        iv = _host_value(vcode, init)
+        check(fn(dtype_code(d_keys_in.dtype), vcode, LCPP_OPS[op], _ptr(temp), _nbytes(temp), _ptr(d_keys_in),
+                 _ptr(d_values_in), _ptr(d_values_out), num_items, ctypes.c_void_p(iv.ctypes.data), _stream(stream)),
+              name)
+
+    def ExclusiveScanByKey(self, temp_storage, d_keys_in, d_values_in, d_values_out, scan_op: str, num_items: int,
+                           initial_value, stream=None):
+        """device_scan.h:206-254: runs of equal consecutive keys; out = initial_value at a head, else
+        scan_op(fold of the run's earlier values, initial_value).  scan_op: "sum" | "min" | "max"."""
+        self._by_key(lib().lcpp_scan_exclusive_by_key, "ExclusiveScanByKey", temp_storage, d_keys_in, d_values_in,
+                     d_values_out, num_items, scan_op, initial_value, stream)
+
+    def InclusiveScanByKey(self, temp_storage, d_keys_in, d_values_in, d_values_out, scan_op: str, num_items: int,
+                           initial_value, stream=None):
+        """device_scan.h:256-303: out = scan_op(fold of the run's values up to i, initial_value)."""
+        self._by_key(lib().lcpp_scan_inclusive_by_key, "InclusiveScanByKey", temp_storage, d_keys_in, d_values_in,
+                     d_values_out, num_items, scan_op, initial_value, stream)
+
+    def ExclusiveSumByKey(self, temp_storage, d_keys_in, d_values_in, d_values_out, num_items: int, stream=None):
+        """device_scan.h:306-322"""
+        self.ExclusiveScanByKey(temp_storage, d_keys_in, d_values_in, d_values_out, "sum", num_items, 0, stream)
+
+    def InclusiveSumByKey(self, temp_storage, d_keys_in, d_values_in, d_values_out, num_items: int, stream=None):
+        """device_scan.h:324-339"""
+        self.InclusiveScanByKey(temp_storage, d_keys_in, d_values_in, d_values_out, "sum", num_items, 0, stream)
 
 
 class DeviceRadixSort:

@@ -917,3 +917,126 @@ int lcor_segment_reduce_mt(int dtype, const void *in, void *out, uint64_t num_se
     for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
     return 0;
 }
+
+/* ======================================================================
+ * Scan by key / reduce by key.
+ *
+ * Segments are maximal runs of consecutive equal keys: element i starts a
+ * segment (a "head") when i == 0 or keys[i] != keys[i-1], the comparison
+ * made in the key's own type, so floating keys treat -0.0 == +0.0 and
+ * NaN != NaN (BlockDiscontinuity::FlagHeads with `a != b`,
+ * block/block_discontinuity.h:97-130; device/details/scan_by_key.h:196-202,
+ * device/details/reduce_by_key.h:168-192).
+ * ====================================================================== */
+static int key_differs(int kd, const void *keys, uint64_t i)
+{
+    switch (kd) {
+    case LCOR_I32: case LCOR_U32: return ((const uint32_t *)keys)[i] != ((const uint32_t *)keys)[i - 1];
+    case LCOR_I64: case LCOR_U64: return ((const uint64_t *)keys)[i] != ((const uint64_t *)keys)[i - 1];
+    case LCOR_F32: return ((const float *)keys)[i] != ((const float *)keys)[i - 1];
+    case LCOR_F64: return ((const double *)keys)[i] != ((const double *)keys)[i - 1];
+    default: return 1;
+    }
+}
+
+/* op(a, b) on one element of dtype dt, into a (integer sums wrap) */
+static void op1(int op, int dt, void *a, const void *b)
+{
+    fold_any(op, dt, b, 1, a);
+}
+
+/* ScanByKey — device/device_scan.h:206-303 (Exclusive/InclusiveScanByKey with
+ * scan_op and init), device/details/scan_by_key.h:77-258 (ScanBySegmentOp
+ * over (head flag, value) pairs, then AddInitToScan):
+ *   exclusive: out[i] = init at a head, else op(fold(values[head..i)), init)
+ *   inclusive: out[i] = op(fold(values[head..i]), init)
+ * The reference's inclusive variant overwrites every head with init
+ * (AddInitToScan, scan_by_key.h:113-128, applied to inclusive results too);
+ * this restatement, like the GPU path, gives heads op(value, init).
+ * Folds run in element order (floating-point results are order-dependent;
+ * lcor_scan_by_key_f64 gives the checker's double-precision values). */
+int lcor_scan_by_key(int inclusive, int op, int key_dtype, int val_dtype, const void *keys,
+                     const void *vals, void *out, uint64_t n, const void *init)
+{
+    const size_t es = dtype_size(val_dtype);
+    if (!dtype_size(key_dtype) || !es || op < 0 || op > 2) return -1;
+    uint64_t run = 0, tmp = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const void *x = (const char *)vals + i * es;
+        char *o = (char *)out + i * es;
+        const int head = i == 0 || key_differs(key_dtype, keys, i);
+        if (head) {
+            if (inclusive) { memcpy(&run, x, es); memcpy(&tmp, &run, es); op1(op, val_dtype, &tmp, init); memcpy(o, &tmp, es); }
+            else { memcpy(o, init, es); memcpy(&run, x, es); }
+        } else {
+            if (inclusive) { op1(op, val_dtype, &run, x); memcpy(&tmp, &run, es); op1(op, val_dtype, &tmp, init); memcpy(o, &tmp, es); }
+            else { memcpy(&tmp, &run, es); op1(op, val_dtype, &tmp, init); memcpy(o, &tmp, es); op1(op, val_dtype, &run, x); }
+        }
+    }
+    return 0;
+}
+
+/* Double-precision segmented sums of floating values (init 0) and the
+ * matching segmented sums of |x|, for the normwise tolerance. */
+int lcor_scan_by_key_f64(int inclusive, int key_dtype, int val_dtype, const void *keys,
+                         const void *vals, double *out, double *abs_prefix, uint64_t n)
+{
+    if (!dtype_size(key_dtype) || (val_dtype != LCOR_F32 && val_dtype != LCOR_F64)) return -1;
+    double s = 0.0, a = 0.0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const double x = val_dtype == LCOR_F32 ? ((const float *)vals)[i] : ((const double *)vals)[i];
+        if (i == 0 || key_differs(key_dtype, keys, i)) { s = 0.0; a = 0.0; }
+        if (!inclusive) { out[i] = s; abs_prefix[i] = a; }
+        s += x;
+        a += fabs(x);
+        if (inclusive) { out[i] = s; abs_prefix[i] = a; }
+    }
+    return 0;
+}
+
+/* ReduceByKey — device/device_reduce.h:277-318, device/details/
+ * reduce_by_key.h:61-258 (ReduceBySegmentOp over (head count, value) pairs,
+ * scatter at heads): run r = r-th maximal run of equal keys;
+ * unique_out[r] = its key, aggregates_out[r] = op-fold of its values (no
+ * init, element order), *num_runs = number of runs (0 when n = 0). */
+int lcor_reduce_by_key(int op, int key_dtype, int val_dtype, const void *keys, const void *vals,
+                       void *unique_out, void *aggregates_out, uint64_t n, uint64_t *num_runs)
+{
+    const size_t ks = dtype_size(key_dtype), es = dtype_size(val_dtype);
+    if (!ks || !es || op < 0 || op > 2) return -1;
+    uint64_t r = 0, acc = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const void *x = (const char *)vals + i * es;
+        if (i > 0 && key_differs(key_dtype, keys, i)) {
+            memcpy((char *)unique_out + r * ks, (const char *)keys + (i - 1) * ks, ks);
+            memcpy((char *)aggregates_out + r * es, &acc, es);
+            ++r;
+        }
+        if (i == 0 || key_differs(key_dtype, keys, i)) memcpy(&acc, x, es);
+        else op1(op, val_dtype, &acc, x);
+    }
+    if (n) {
+        memcpy((char *)unique_out + r * ks, (const char *)keys + (n - 1) * ks, ks);
+        memcpy((char *)aggregates_out + r * es, &acc, es);
+        ++r;
+    }
+    *num_runs = r;
+    return 0;
+}
+
+/* Double-precision run sums of floating values and run sums of |x|. */
+int lcor_reduce_by_key_f64(int key_dtype, int val_dtype, const void *keys, const void *vals,
+                           uint64_t n, double *sums, double *abs_sums, uint64_t *num_runs)
+{
+    if (!dtype_size(key_dtype) || (val_dtype != LCOR_F32 && val_dtype != LCOR_F64)) return -1;
+    uint64_t r = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const double x = val_dtype == LCOR_F32 ? ((const float *)vals)[i] : ((const double *)vals)[i];
+        if (i > 0 && key_differs(key_dtype, keys, i)) ++r;
+        if (i == 0 || key_differs(key_dtype, keys, i)) { sums[r] = 0.0; abs_sums[r] = 0.0; }
+        sums[r] += x;
+        abs_sums[r] += fabs(x);
+    }
+    *num_runs = n ? r + 1 : 0;
+    return 0;
+}

@@ -31,6 +31,12 @@
  *                   checker (planted-mistake tests)
  *   segment reduce  numpy per-segment sums, reference KAT (1024 shuffled ints,
  *                   segments of 100, std::accumulate golden)
+ *   scan by key     numpy cumsum differences inside runs (wraparound), single
+ *                   run == plain scan, all-distinct keys == init / op(x, init),
+ *                   reference KAT (keys i/100, ones -> i % 100)
+ *   reduce by key   numpy add/minimum/maximum.reduceat over run heads, run
+ *                   count from np.diff, reference KAT (keys i/100 over the
+ *                   shuffled 0..4095 golden -> chunk sums)
  */
 #ifndef LCPP_ORACLE_H
 #define LCPP_ORACLE_H
@@ -94,6 +100,17 @@ int lcor_check_stable_pairs_u64_u32(const uint64_t *keys_in, const uint64_t *key
                                     const uint32_t *vals_out, uint64_t n);
 int lcor_check_sorted_permutation_u32(const uint32_t *keys_in, const uint32_t *keys_out,
                                       uint64_t n);
+
+/* ---------------- scan by key / reduce by key -------------------------- */
+/* heads: i == 0 or keys[i] != keys[i-1] (compared in the key type) */
+int lcor_scan_by_key(int inclusive, int op, int key_dtype, int val_dtype, const void *keys,
+                     const void *vals, void *out, uint64_t n, const void *init);
+int lcor_scan_by_key_f64(int inclusive, int key_dtype, int val_dtype, const void *keys,
+                         const void *vals, double *out, double *abs_prefix, uint64_t n);
+int lcor_reduce_by_key(int op, int key_dtype, int val_dtype, const void *keys, const void *vals,
+                       void *unique_out, void *aggregates_out, uint64_t n, uint64_t *num_runs);
+int lcor_reduce_by_key_f64(int key_dtype, int val_dtype, const void *keys, const void *vals,
+                           uint64_t n, double *sums, double *abs_sums, uint64_t *num_runs);
 
 /* ---------------- segment reduce -------------------------------------- */
 int lcor_segment_reduce(int op, int dtype, const void *in, void *out, uint64_t num_segments,

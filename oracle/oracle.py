@@ -63,6 +63,10 @@ def lib() -> ctypes.CDLL:
             "lcor_radix_sort": (i, [i, i, vp, vp, vp, vp, u64, i, i, u32]),
             "lcor_check_stable_pairs_u64_u32": (i, [vp, vp, vp, u64]),
             "lcor_check_sorted_permutation_u32": (i, [vp, vp, u64]),
+            "lcor_scan_by_key": (i, [i, i, i, i, vp, vp, vp, u64, vp]),
+            "lcor_scan_by_key_f64": (i, [i, i, i, vp, vp, vp, vp, u64]),
+            "lcor_reduce_by_key": (i, [i, i, i, vp, vp, vp, vp, u64, ctypes.POINTER(u64)]),
+            "lcor_reduce_by_key_f64": (i, [i, i, vp, vp, u64, vp, vp, ctypes.POINTER(u64)]),
             "lcor_segment_reduce": (i, [i, i, vp, vp, u64, vp, vp]),
             "lcor_segment_reduce_f64": (i, [i, vp, u64, vp, vp, vp, vp]),
             "lcor_segment_reduce_mt": (i, [i, vp, vp, u64, vp, vp, i]),
@@ -218,6 +222,53 @@ def check_stable_pairs_u64_u32(keys_in, keys_out, vals_out) -> bool:
 
 def check_sorted_permutation_u32(keys_in, keys_out) -> bool:
     return lib().lcor_check_sorted_permutation_u32(_p(keys_in), _p(keys_out), keys_in.size) == 1
+
+
+# ---------------------------------------------------------------- by key
+def scan_by_key(keys: np.ndarray, values: np.ndarray, inclusive: bool, op: int = OP_SUM, init=0) -> np.ndarray:
+    """ScanByKey over runs of equal consecutive keys (exclusive: init at heads)."""
+    keys = np.ascontiguousarray(keys)
+    values = np.ascontiguousarray(values)
+    out = np.empty_like(values)
+    iv = np.array([init], dtype=values.dtype)
+    _ok(lib().lcor_scan_by_key(int(inclusive), op, _code(keys), _code(values), _p(keys), _p(values), _p(out),
+                               values.size, _p(iv)), "scan_by_key")
+    return out
+
+
+def scan_by_key_f64(keys: np.ndarray, values: np.ndarray, inclusive: bool):
+    """(double-precision segmented prefix sums, segmented prefix sums of |x|)."""
+    keys = np.ascontiguousarray(keys)
+    values = np.ascontiguousarray(values)
+    out = np.empty(values.size, np.float64)
+    ab = np.empty(values.size, np.float64)
+    _ok(lib().lcor_scan_by_key_f64(int(inclusive), _code(keys), _code(values), _p(keys), _p(values), _p(out),
+                                   _p(ab), values.size), "scan_by_key_f64")
+    return out, ab
+
+
+def reduce_by_key(keys: np.ndarray, values: np.ndarray, op: int = OP_SUM):
+    """(unique keys, aggregates) of the runs of equal consecutive keys."""
+    keys = np.ascontiguousarray(keys)
+    values = np.ascontiguousarray(values)
+    uk = np.empty_like(keys)
+    ag = np.empty_like(values)
+    runs = ctypes.c_uint64()
+    _ok(lib().lcor_reduce_by_key(op, _code(keys), _code(values), _p(keys), _p(values), _p(uk), _p(ag), values.size,
+                                 ctypes.byref(runs)), "reduce_by_key")
+    return uk[: runs.value], ag[: runs.value]
+
+
+def reduce_by_key_f64(keys: np.ndarray, values: np.ndarray):
+    """(double-precision run sums, run sums of |x|)."""
+    keys = np.ascontiguousarray(keys)
+    values = np.ascontiguousarray(values)
+    s = np.empty(max(values.size, 1), np.float64)
+    ab = np.empty(max(values.size, 1), np.float64)
+    runs = ctypes.c_uint64()
+    _ok(lib().lcor_reduce_by_key_f64(_code(keys), _code(values), _p(keys), _p(values), values.size, _p(s), _p(ab),
+                                     ctypes.byref(runs)), "reduce_by_key_f64")
+    return s[: runs.value], ab[: runs.value]
 
 
 # ---------------------------------------------------------------- segment reduce

@@ -83,6 +83,17 @@ def test_temp_bytes_queries(L):
     assert rc == 0 and b == 4 * 256 * 4 + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 4 + (1 << 28) * 4
     rc, bp = _q(L.lcpp_radix_sort_pairs_temp_bytes, 4, 1, 1 << 27)
     assert rc == 0 and bp > (1 << 27) * 12
+    # scan by key: one packed word per 8192-value tile (two for 8-byte values)
+    rc, b = _q(L.lcpp_scan_by_key_temp_bytes, 0, 2, 1 << 28)
+    assert rc == 0 and b == (1 << 15) * 8
+    rc, b = _q(L.lcpp_scan_by_key_temp_bytes, 2, 5, 1 << 27)
+    assert rc == 0 and b == (1 << 15) * 16
+    # reduce by key: head-count words + open-run words, each 256-byte aligned
+    rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 0, 0, 1 << 28)
+    assert rc == 0 and b == 2 * (1 << 15) * 8
+    rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 5, 5, 100)
+    assert rc == 0 and b == 256 + 256
+    assert _q(L.lcpp_reduce_by_key_temp_bytes, 0, 9, 100)[0] == -3
     # segment reduce needs none (as the reference)
     assert _q(L.lcpp_segment_reduce_temp_bytes, 2, 1 << 20) == (0, 0)
 
@@ -106,10 +117,18 @@ def test_unsupported_dtype_and_null_args(L):
     assert L.lcpp_radix_sort_pairs_descending(1, 9, None, 0, None, None, None, None, 10, None) == -3
     assert L.lcpp_radix_sort_pairs_descending(4, 1, None, 0, None, None, None, None, 10, None) == -1
     assert L.lcpp_segment_reduce_sum(2, None, 0, None, None, 10, None, None, None) == -1
+    assert L.lcpp_scan_exclusive_by_key(0, 0, 0, None, 0, None, None, None, 10, None, None) == -1
+    assert L.lcpp_scan_inclusive_by_key(0, 0, 5, None, 0, None, None, None, 10, None, None) == -1  # bad op
+    assert L.lcpp_scan_inclusive_sum_by_key(9, 0, None, 0, None, None, None, 10, None) == -3
+    assert L.lcpp_scan_exclusive_sum_by_key(0, 9, None, 0, None, None, None, 10, None) == -3
+    assert L.lcpp_reduce_by_key(0, 0, 0, None, 0, None, None, None, None, None, 10, None) == -1
+    assert L.lcpp_reduce_by_key(0, 0, 7, None, 0, None, None, None, None, None, 10, None) == -1
+    assert L.lcpp_reduce_by_key(0, 9, 0, None, 0, None, None, None, None, None, 10, None) == -3
     # zero-sized work is a no-op success
     assert L.lcpp_scan_inclusive_sum(0, None, 0, None, None, 0, None) == 0
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 0, None) == 0
     assert L.lcpp_segment_reduce_sum(2, None, 0, None, None, 0, None, None, None) == 0
+    assert L.lcpp_scan_exclusive_sum_by_key(0, 0, None, 0, None, None, None, 0, None) == 0
 
 
 def test_temp_too_small_detected_before_launch(L):
@@ -117,6 +136,9 @@ def test_temp_too_small_detected_before_launch(L):
     assert L.lcpp_scan_exclusive_sum(1, dummy, 16, dummy, dummy, 1 << 20, None) == -2
     assert L.lcpp_radix_sort_keys(1, dummy, 16, dummy, dummy, 1 << 20, None) == -2
     assert L.lcpp_reduce_sum(0, dummy, 16, dummy, dummy, 1 << 28, None) == -2
+    assert L.lcpp_scan_inclusive_sum_by_key(0, 0, dummy, 16, dummy, dummy, dummy, 1 << 20, None) == -2
+    assert L.lcpp_reduce_by_key(0, 0, 0, dummy, 16, dummy, dummy, dummy, dummy, dummy, 1 << 20, None) == -2
+    assert L.lcpp_reduce_by_key(0, 0, 0, dummy, 1 << 30, dummy, dummy, dummy, dummy, dummy, 1 << 32, None) == -1
 
 
 def test_misaligned_temp_rejected(L):
@@ -125,10 +147,50 @@ def test_misaligned_temp_rejected(L):
     assert L.lcpp_scan_exclusive_sum(1, p, b, p, p, 1 << 20, None) == -1
 
 
+CPP_USE = r"""
+#include "lcpp/parallel_primitive.h"
+using namespace luisa::parallel_primitive;
+int main()
+{
+    CommandList cl{};
+    BufferView<uint> temp{};
+    BufferView<int> ki{}, ko{}, vi{}, vo{};
+    BufferView<float> fi{}, fo{};
+    BufferView<uint> runs{}, idx{}, beg{}, end{};
+    DeviceReduce<> r;
+    r.Sum(cl, temp, vi, vo, 10);
+    r.Min(cl, temp, vi, vo, 10);
+    r.Max(cl, temp, vi, vo, 10);
+    r.ArgMin(cl, temp, vi, vo, idx, 10);
+    r.ArgMax(cl, temp, vi, vo, idx, 10);
+    r.TransformReduce(cl, temp, fi, fo, 10, SumOp{}, SquareOp{}, 0.f);
+    r.ReduceByKey(cl, temp, ki, fi, ko, fo, runs, MaxOp{}, 10);
+    DeviceScan<> s;
+    s.ExclusiveSum(cl, temp, vi, vo, 10);
+    s.InclusiveSum(cl, temp, fi, fo, 10);
+    s.ExclusiveScanByKey(cl, temp, ki, fi, fo, MinOp{}, 10, 1.f);
+    s.InclusiveScanByKey(cl, temp, ki, vi, vo, SumOp{}, 10, 0);
+    s.ExclusiveSumByKey(cl, temp, ki, vi, vo, 10);
+    s.InclusiveSumByKey(cl, temp, ki, vi, vo, 10);
+    DeviceRadixSort<> rs;
+    rs.SortKeys(cl, temp, ki, ko, 10u);
+    rs.SortPairs(cl, temp, ki, ko, fi, fo, 10u);
+    rs.SortKeysDescending(cl, temp, ki, ko, 10u);
+    rs.SortPairsDescending(cl, temp, ki, ko, fi, fo, 10u);
+    DeviceSegmentReduce<> sr;
+    sr.Sum(cl, temp, fi, fo, 10u, beg, end);
+    return (int)(DeviceReduce<>::GetTempStorageBytes<int>(10) + DeviceScan<>::GetScanByKeyTempStorageBytes<int, float>(10) +
+                 DeviceReduce<>::GetReduceByKeyTempStorageBytes<int, float>(10) +
+                 DeviceRadixSort<>::GetSortPairsTempStorageBytes<int, float>(10u) +
+                 DeviceSegmentReduce<>::GetTempStorageBytes<float>(10));
+}
+"""
+
+
 def test_cpp_host_api_compiles():
     """include/lcpp/parallel_primitive.h (the reference's class names over the
-    C ABI) is valid C++17 on its own."""
-    src = '#include "lcpp/parallel_primitive.h"\nint main(){return 0;}\n'
+    C ABI) is valid C++17 and every method template instantiates."""
+    src = CPP_USE
     r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
                         "-x", "c++", "-"], input=src, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr

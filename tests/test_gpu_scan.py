@@ -95,3 +95,31 @@ def test_full_size_f32_inclusive(gpu):
     ab = np.cumsum(np.abs(h))
     err = np.abs(got.astype(np.float64) - ref)
     assert (err <= RTOL_SCAN * ab).all(), float((err / ab).max())
+
+
+@pytest.mark.parametrize("dtype", [np.uint32, np.int64])
+@pytest.mark.parametrize("n", [5, 16383, 16385, 3 * 16384 + 7])
+@pytest.mark.parametrize("pad", [0, 1])
+def test_ragged_tile_writes_nothing_past_the_end(gpu, dtype, n, pad):
+    """The last tile's element-wise path stores only [0, n): the output's
+    trailing guard (and the input's, so every access stays inside allocated
+    memory even past n) keeps its fill value."""
+    import gpu_util as g
+    import torch
+
+    guard = 1 << 15  # > one tile of elements
+    a = g.random_array(dtype, n, seed=n)
+    din = g.empty(n + guard, dtype, pad=pad)
+    din[:n].copy_(torch.from_numpy(a))
+    din[n:].fill_(1)
+    for kind, incl in (("ExclusiveSum", False), ("InclusiveSum", True)):
+        log(f"scan guard {kind} {np.dtype(dtype).name} n={n} pad={pad}")
+        out = g.empty(n + guard, dtype, pad=pad)
+        out.fill_(77)
+        from lc_parallel_primitive_amd import DeviceScan
+
+        tmp = g.temp(DeviceScan.GetTempStorageBytes(np.dtype(dtype).name, n))
+        getattr(DeviceScan(), kind)(tmp, din, out, n)
+        h = g.to_host(out)
+        assert (h[:n] == o.scan(a, incl)).all()
+        assert (h[n:] == 77).all(), "store past the end of the output"

@@ -368,3 +368,160 @@ def test_segment_reduce_empty_and_inverted_segments():
     b = np.array([0, 3, 3, 7, 9], np.uint32)
     e = np.array([3, 3, 1, 10, 9], np.uint32)  # [0,3), empty, inverted (empty), [7,10), empty
     assert list(o.segment_reduce(o.OP_SUM, a, b, e)) == [3, 0, 0, 24, 0]
+
+
+# ------------------------------------------------------------------ scan by key / reduce by key
+BYKEY_VALUE_DTYPES = [np.int32, np.uint32, np.int64, np.uint64]
+
+
+def run_keys(n: int, mean_len: float, seed: int, dtype=np.int32) -> np.ndarray:
+    """Keys made of runs with geometric lengths (consecutive runs differ)."""
+    rng = np.random.default_rng(seed)
+    heads = rng.random(n) < 1.0 / mean_len
+    heads[0] = True
+    return (np.cumsum(heads) * 7 % 1000).astype(dtype)
+
+
+def heads_of(keys: np.ndarray) -> np.ndarray:
+    h = np.ones(keys.size, bool)
+    h[1:] = keys[1:] != keys[:-1]
+    return h
+
+
+def np_scan_by_key_sum(keys, v, inclusive, init):
+    """Segmented sums as differences of one global cumsum (wraparound in the
+    element type): independent of the oracle's per-element restart."""
+    with np.errstate(over="ignore"):
+        c = np.cumsum(v, dtype=v.dtype)
+        start = np.maximum.accumulate(np.where(heads_of(keys), np.arange(v.size), 0))
+        base = np.where(start > 0, c[np.maximum(start - 1, 0)], v.dtype.type(0)).astype(v.dtype)
+        incl = (c - base).astype(v.dtype)
+        out = incl if inclusive else (incl - v).astype(v.dtype)
+        return (out + v.dtype.type(init)).astype(v.dtype)
+
+
+def test_scan_by_key_kat_exclusive_ones():
+    # device_scan_test.cpp:111-167: keys i/100, values 1 -> i % 100
+    for k in range(5, 17):
+        n = 1 << k
+        keys = (np.arange(n) // 100).astype(np.int32)
+        got = o.scan_by_key(keys, np.ones(n, np.int32), inclusive=False)
+        assert (got == np.arange(n) % 100).all()
+
+
+@pytest.mark.parametrize("dt", BYKEY_VALUE_DTYPES)
+@pytest.mark.parametrize("inclusive", [False, True])
+def test_scan_by_key_sum_vs_numpy_cumsum_differences(dt, inclusive):
+    n = 50_000
+    keys = run_keys(n, 37, 5)
+    info = np.iinfo(dt)
+    v = np.random.default_rng(6).integers(info.min, info.max, n, dtype=dt, endpoint=True)
+    for init in (0, 12345):
+        got = o.scan_by_key(keys, v, inclusive, o.OP_SUM, init)
+        assert (got == np_scan_by_key_sum(keys, v, inclusive, init)).all()
+
+
+@pytest.mark.parametrize("op", [o.OP_MIN, o.OP_MAX])
+@pytest.mark.parametrize("inclusive", [False, True])
+def test_scan_by_key_min_max_vs_numpy_accumulate(op, inclusive):
+    n = 20_000
+    keys = run_keys(n, 25, 7, np.uint32)
+    v = np.random.default_rng(8).integers(-10**6, 10**6, n).astype(np.int32)
+    init = np.int32(500_000 if op == o.OP_MIN else -500_000)
+    npop = np.minimum if op == o.OP_MIN else np.maximum
+    ref = np.empty_like(v)
+    h = np.flatnonzero(heads_of(keys))
+    for s, e in zip(h, list(h[1:]) + [n]):
+        acc = npop.accumulate(v[s:e])
+        if inclusive:
+            ref[s:e] = npop(acc, init)
+        else:
+            ref[s] = init
+            ref[s + 1:e] = npop(acc[:-1], init)
+    assert (o.scan_by_key(keys, v, inclusive, op, init) == ref).all()
+
+
+def test_scan_by_key_special_cases():
+    v = o.gen("reduce_i32", 4097, 11)
+    one_run = np.full(v.size, 9, np.int64)
+    for inclusive in (False, True):
+        assert (o.scan_by_key(one_run, v, inclusive) == o.scan(v, inclusive)).all()
+    distinct = np.arange(v.size, dtype=np.uint64)
+    assert (o.scan_by_key(distinct, v, False, o.OP_SUM, 3) == 3).all()
+    assert (o.scan_by_key(distinct, v, True, o.OP_SUM, 3) == v + 3).all()
+    assert (o.scan_by_key(distinct, v, True, o.OP_MAX, 0) == np.maximum(v, 0)).all()
+    assert o.scan_by_key(np.empty(0, np.int32), np.empty(0, np.int32), True).size == 0
+
+
+def test_scan_by_key_float_key_equality():
+    # keys compared as floats: -0.0 == +0.0 (one run), NaN != NaN (each its own run)
+    keys = np.array([1.0, -0.0, 0.0, np.nan, np.nan, 2.0], np.float32)
+    v = np.ones(6, np.int32)
+    assert list(o.scan_by_key(keys, v, True)) == [1, 1, 2, 1, 1, 1]
+    uk, ag = o.reduce_by_key(keys, v)
+    assert list(ag) == [1, 2, 1, 1, 1] and uk.size == 5
+
+
+def test_scan_by_key_f64_and_float_values():
+    n = 30_000
+    keys = run_keys(n, 50, 12, np.float64)
+    f = o.gen("normal_f32", n, 13)
+    for inclusive in (False, True):
+        s, ab = o.scan_by_key_f64(keys, f, inclusive)
+        ref = np_scan_by_key_sum(keys, f.astype(np.float64), inclusive, 0)
+        np.testing.assert_allclose(s, ref, rtol=0, atol=1e-9)
+        got = o.scan_by_key(keys, f, inclusive).astype(np.float64)
+        assert (np.abs(got - s) <= 1e-5 * ab + 1e-30).all()
+
+
+def test_scan_by_key_planted_missing_head_is_caught():
+    keys = run_keys(5000, 20, 14)
+    v = np.ones(5000, np.int32)
+    good = o.scan_by_key(keys, v, True)
+    bad_keys = keys.copy()
+    h = np.flatnonzero(heads_of(keys))
+    bad_keys[h[10]] = bad_keys[h[10] - 1]  # merge two runs at one position
+    assert not (np_scan_by_key_sum(bad_keys, v, True, 0) == good).all()
+
+
+def test_reduce_by_key_kat_shuffled_chunks():
+    # device_reduce_test.cpp:229-289: keys i/100 over the shuffled 0..4095
+    a = golden("reduce_shuffled_4096_i32.bin", np.int32)
+    keys = (np.arange(a.size) // 100).astype(np.int32)
+    uk, ag = o.reduce_by_key(keys, a)
+    assert uk.size == 41 and (uk == np.arange(41)).all()
+    assert (ag == np.array([a[i * 100:(i + 1) * 100].sum() for i in range(41)])).all()
+
+
+@pytest.mark.parametrize("dt", BYKEY_VALUE_DTYPES + [np.float32, np.float64])
+@pytest.mark.parametrize("op", [o.OP_SUM, o.OP_MIN, o.OP_MAX])
+def test_reduce_by_key_vs_numpy_reduceat(dt, op):
+    n = 40_000
+    keys = run_keys(n, 9, 15, np.int64)
+    dt = np.dtype(dt)
+    if dt.kind == "f":
+        v = np.random.default_rng(16).integers(-1000, 1000, n).astype(dt)  # exact in any order
+    else:
+        info = np.iinfo(dt)
+        v = np.random.default_rng(16).integers(info.min, info.max, n, dtype=dt, endpoint=True)
+    h = np.flatnonzero(heads_of(keys))
+    npop = {o.OP_SUM: np.add, o.OP_MIN: np.minimum, o.OP_MAX: np.maximum}[op]
+    with np.errstate(over="ignore"):
+        ref = npop.reduceat(v, h).astype(dt)
+    uk, ag = o.reduce_by_key(keys, v, op)
+    assert uk.size == h.size == 1 + np.count_nonzero(np.diff(keys))
+    assert (uk == keys[h]).all() and (ag == ref).all()
+
+
+def test_reduce_by_key_f64_and_edges():
+    n = 20_000
+    keys = run_keys(n, 3, 17, np.uint32)
+    f = o.gen("normal_f32", n, 18)
+    s, ab = o.reduce_by_key_f64(keys, f)
+    h = np.flatnonzero(heads_of(keys))
+    np.testing.assert_allclose(s, np.add.reduceat(f.astype(np.float64), h), rtol=0, atol=1e-9)
+    assert (ab >= np.abs(s)).all()
+    uk, ag = o.reduce_by_key(np.empty(0, np.int32), np.empty(0, np.int32))
+    assert uk.size == 0 and ag.size == 0
+    uk, ag = o.reduce_by_key(np.array([5], np.int32), np.array([-7], np.int32))
+    assert list(uk) == [5] and list(ag) == [-7]
