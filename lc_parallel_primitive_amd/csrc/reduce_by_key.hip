@@ -150,8 +150,11 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
                 const uint32_t gi = base + e;
                 const bool h = ((fl >> (k * VP + j)) & 1u) != 0;
                 const V x = r.val[k][j];
+                // run indices are < n by construction; the bound keeps a
+                // broken invariant (a look-back wait past its spin limit)
+                // from ever writing outside the outputs
                 if (h) {
-                    if (gi > 0) {
+                    if (gi > 0 && c - 1 < n) {
                         unique_out[c - 1] = j > 0 ? r.key[k][j - 1] : prev0[k];
                         agg_out[c - 1] = s;
                     }
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
                 } else {
                     s = op(s, x);
                 }
-                if (gi == n - 1) {
+                if (gi == n - 1 && c - 1 < n) {
                     unique_out[c - 1] = r.key[k][j];
                     agg_out[c - 1] = s;
                     *num_runs = c;
