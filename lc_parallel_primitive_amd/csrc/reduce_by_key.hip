@@ -57,7 +57,6 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
     __shared__ uint32_t s_F[kBkVecs];
     __shared__ V s_vprefix;
     __shared__ uint32_t s_cprefix;
-    __shared__ uint32_t s_first_head;
 
     Op op;
     const V ident = op_identity<Op, V>();
@@ -72,7 +71,6 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
     if (tid < kBkVecs) s_F[tid] = 0;
     K prev0[kBkVecs];
     const uint32_t fl = bk_heads<K, VP>(r.key, prev0, s_last, s_pred, keys, base, tile, tid);
-    if (tid == 0) s_first_head = fl & 1u;
 
     // pass 1: per vector, (has-head, open fold) pairs and head counts, wave
     // scans of both, wave totals to LDS
@@ -109,7 +107,9 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
         for (int k = 0; k < kBkVecs; ++k)
 #pragma unroll
             for (int w = 0; w < kBkWaves; ++w) seg_fold(tf, ts, ((s_F[k] >> w) & 1u) != 0, s_S[k][w], op);
-        const V p = lb_segmented_tile(vwords, tile, ts, tf, s_first_head == 0, op, ident);
+        // always wait: a head at the tile's first element closes the run the
+        // previous tile left open, whose aggregate is exactly this prefix
+        const V p = lb_segmented_tile(vwords, tile, ts, tf, true, op, ident);
         if (lane == 0) s_vprefix = p;
     } else if (wave == 1) {
         uint32_t tc = 0;

@@ -106,7 +106,7 @@ def test_kat_reduce_by_key_shuffled(gpu):
 @pytest.mark.parametrize("vdt", VAL_DTYPES)
 def test_scan_by_key_dtypes(gpu, kdt, vdt):
     n = 50_003
-    for mean in (2.5, 300, 20_000):
+    for mean in (1.5, 300, 20_000):
         keys = run_keys(n, mean, 1, kdt)
         v = values(vdt, n, 2)
         for inclusive in (False, True):
