@@ -258,6 +258,33 @@ def main():
                                                     ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(vo.data_ptr()),
                                                     n, sp), "pairs"), 5, "rs_onesweep", items=n)
             del k, v, ko, vo, t1
+        if want("by_key"):
+            n = 1 << 28
+            k = datagen.run_keys_i32(n, 7)
+            runs = int(k[-1].item()) - int(k[0].item()) + 1
+            x = datagen.normal_f32(n, seed=datagen.SEED_SEG_VALUES)
+            y = torch.empty_like(x)
+            tb = tmp_bytes(L.lcpp_scan_by_key_temp_bytes, I32, F32, n)
+            t1 = torch.empty(tb, dtype=torch.uint8, device="cuda")
+            add("DeviceScan::InclusiveSumByKey int32 keys (runs of mean 128) -> float32 N=2^28", 12 * n,
+                lambda: chk(L.lcpp_scan_inclusive_sum_by_key(I32, F32, ctypes.c_void_p(t1.data_ptr()), tb,
+                                                             ctypes.c_void_p(k.data_ptr()),
+                                                             ctypes.c_void_p(x.data_ptr()),
+                                                             ctypes.c_void_p(y.data_ptr()), n, sp), "sbk"),
+                20, "scan_by_key_inclusive")
+            del y, t1
+            uk = torch.empty_like(k)
+            ag = torch.empty_like(x)
+            nr = torch.zeros(1, dtype=torch.int32, device="cuda")
+            tb = tmp_bytes(L.lcpp_reduce_by_key_temp_bytes, I32, F32, n)
+            t1 = torch.empty(tb, dtype=torch.uint8, device="cuda")
+            add("DeviceReduce::ReduceByKey sum int32 keys (runs of mean 128) -> float32 N=2^28", 8 * n + 8 * runs,
+                lambda: chk(L.lcpp_reduce_by_key(I32, F32, 0, ctypes.c_void_p(t1.data_ptr()), tb,
+                                                 ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                                 ctypes.c_void_p(uk.data_ptr()), ctypes.c_void_p(ag.data_ptr()),
+                                                 ctypes.c_void_p(nr.data_ptr()), n, sp), "rbk"),
+                20, "reduce_by_key")
+            del k, x, uk, ag, t1
         if want("segment"):
             n, S = 1 << 27, 1 << 20
             x = datagen.normal_f32(n, seed=datagen.SEED_SEG_VALUES)

@@ -14,9 +14,9 @@
 // (single_pass_scan_operator.h:81-93); release/acquire pairs instead cost
 // an L2 write-back/invalidate per publish on this part.
 //
-// The prefix wait is executed by all 64 lanes of one wave: lane l polls
-// predecessor top - l, all loads issued before any wait, and the wave stops
-// at the nearest INCLUSIVE tile, waiting only for closer predecessors.
+// The prefix wait is executed by one wave: lane l < 16 polls predecessor
+// top - l, all loads issued before any wait, and the wave stops at the
+// nearest INCLUSIVE tile, waiting only for closer predecessors.
 #pragma once
 
 #include "common.hpp"
@@ -56,6 +56,14 @@ __device__ __forceinline__ void lb_publish(uint64_t *words, uint32_t tile, T v, 
     }
 }
 
+// Predecessors polled per round trip.  A poll is an agent-scope load that
+// is served past the XCD's L2; under full HBM load the polls of ~1000
+// resident tiles compete with the data stream.  Measured at 2^28 (us per
+// scan, u32): 64 lanes 423, 32 lanes 386, 16 lanes 371, 8 lanes 383, 4
+// lanes 387 (a 16-word window is one 128-byte line of 8-byte words).
+// Polling 2 or 4 windows of 64 per round trip: 488 / 565 us.
+constexpr int kLbPollWidth = 16;
+
 // Exclusive prefix of `tile` (tile > 0): the op-fold of the aggregates of
 // the tiles after the nearest INCLUSIVE predecessor, folded onto that
 // predecessor's inclusive value.  Every lane returns it.  `op` must be
@@ -68,10 +76,12 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
     int64_t top = (int64_t)tile - 1;
     uint32_t spins = 0;
     for (;;) {
-        // Lane l polls predecessor top - l.  The load is unconditional (an
-        // index below 0 reads word 0 and is then treated as INCLUSIVE
-        // identity), so the compiler issues it without a branch around it.
-        const int64_t j = top - (int64_t)lane;
+        // Lane l < kLbPollWidth polls predecessor top - l; the other lanes
+        // re-read lane 0's word (same cache line) and are neutral.  The load
+        // is unconditional (an index below 0 reads word 0 and is then treated
+        // as INCLUSIVE identity), so no branch separates issue and wait.
+        const bool poller = lane < (uint32_t)kLbPollWidth;
+        const int64_t j = top - (int64_t)(poller ? lane : 0u);
         const uint64_t jj = j < 0 ? 0 : (uint64_t)j;
         uint32_t s;
         T v;
@@ -89,6 +99,10 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
             s = kStInclusive;
             v = identity;
         }
+        if (!poller) {
+            s = kStPartial;
+            v = identity;
+        }
         const uint64_t incl = ballot(s == kStInclusive);
         const uint32_t stop = incl ? (uint32_t)__builtin_ctzll(incl) : (uint32_t)(kWave - 1);
         const bool in_range = lane <= stop;
@@ -96,9 +110,11 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
             __builtin_amdgcn_s_sleep(1);
             continue;  // re-poll the same window
         }
-        excl = op(excl, wave_allreduce(in_range ? v : identity, op));
-        if (incl) break;
-        top -= kWave;
+        const T acc = in_range ? v : identity;
+        const bool found = incl != 0;
+        excl = op(excl, wave_allreduce(acc, op));
+        if (found) break;
+        top -= kLbPollWidth;
     }
     return excl;
 }

@@ -28,7 +28,7 @@
 //  * Look-back (lookback.hpp): one self-validating packed word per tile
 //    (two for 64-bit types) written with agent-scope relaxed stores
 //    (release/acquire pairs cost an L2 write-back/invalidate per publish on
-//    this part: 7.8 ms for 2^27 x 64-bit); wave 0 polls 64 predecessors at
+//    this part: 7.8 ms for 2^27 x 64-bit); wave 0 polls 16 predecessors at
 //    once and stops at the nearest INCLUSIVE.
 #include "lookback.hpp"
 

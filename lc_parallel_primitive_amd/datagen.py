@@ -113,6 +113,21 @@ def keys_u64_low16(n: int, seed: int = SEED_PAIRS_U64, device="cuda"):
     return t
 
 
+SEED_BY_KEY = 0xB1
+
+
+def run_keys_i32(n: int, log2_mean: int = 7, seed: int = SEED_BY_KEY, device="cuda"):
+    """Keys made of runs of equal values with geometric lengths of mean
+    2^log2_mean: key_i = #{j <= i : lo32(w_j) mod 2^log2_mean == 0}
+    (int32; the host regenerates it from the same splitmix64 stream)."""
+    import torch
+
+    w = keys_u32(n, seed, device)
+    heads = (w.view(torch.int32) & ((1 << log2_mean) - 1)) == 0
+    del w
+    return torch.cumsum(heads, dim=0, dtype=torch.int32)
+
+
 def iota_u32(n: int, device="cuda"):
     import torch
 
