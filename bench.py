@@ -296,7 +296,7 @@ def main():
                 lambda: chk(L.lcpp_segment_reduce_sum(F32, None, 0, ctypes.c_void_p(x.data_ptr()),
                                                       ctypes.c_void_p(y.data_ptr()), S, ctypes.c_void_p(db.data_ptr()),
                                                       ctypes.c_void_p(de.data_ptr()), sp), "segment"), 20,
-                "segment_sum")
+                "segment_reduce")
             del x, y, db, de
         result["secondary"] = sec
 

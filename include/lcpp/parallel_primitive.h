@@ -29,6 +29,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <limits>
 #include <type_traits>
 
 #include "../lcpp_amd.h"
@@ -374,7 +375,8 @@ class DeviceRadixSort : public LuisaModule {
     }
 };
 
-/* device/device_segment_reduce.h:26-135 */
+/* device/device_segment_reduce.h:26-349.  Overloads take CSR begin/end offsets or a fixed
+ * segment_size, as the reference's do. */
 template <size_t BLOCK_SIZE = details::BLOCK_SIZE, size_t WARP_NUMS = details::WARP_SIZE,
           size_t ITEMS_PER_THREAD = details::ITEMS_PER_THREAD>
 class DeviceSegmentReduce : public LuisaModule {
@@ -386,6 +388,35 @@ class DeviceSegmentReduce : public LuisaModule {
         lcpp_segment_reduce_temp_bytes(dtype_of<T>(), 0, &b);
         return b;
     }
+    /* device/device_segment_reduce.h:77-89 */
+    template <class T>
+    static size_t GetArgTempStorageBytes(size_t num_item, size_t num_segments)
+    {
+        size_t b = 0;
+        lcpp_segment_reduce_arg_temp_bytes(dtype_of<T>(), num_item, num_segments, &b);
+        return b;
+    }
+    /* device/device_segment_reduce.h:94-107 (reduce_op: SumOp, MinOp or MaxOp) */
+    template <class T, class ReduceOp>
+    void Reduce(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                uint num_segments, BufferView<uint> d_begin_offsets, BufferView<uint> d_end_offsets, ReduceOp,
+                T initial_value)
+    {
+        check(lcpp_segment_reduce(dtype_of<T>(), reduce_op_of<ReduceOp>(), temp_storage.data(),
+                                  temp_storage.size_bytes(), d_in.data(), d_out.data(), num_segments,
+                                  d_begin_offsets.data(), d_end_offsets.data(), &initial_value, cmdlist.stream),
+              "DeviceSegmentReduce::Reduce");
+    }
+    /* device/device_segment_reduce.h:109-123 */
+    template <class T, class ReduceOp>
+    void Reduce(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                uint num_segments, uint segment_size, ReduceOp, T initial_value)
+    {
+        check(lcpp_segment_reduce_fixed(dtype_of<T>(), reduce_op_of<ReduceOp>(), temp_storage.data(),
+                                        temp_storage.size_bytes(), d_in.data(), d_out.data(), num_segments,
+                                        segment_size, &initial_value, cmdlist.stream),
+              "DeviceSegmentReduce::Reduce");
+    }
     template <class T>
     void Sum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
              uint num_segments, BufferView<uint> d_begin_offsets, BufferView<uint> d_end_offsets)
@@ -394,6 +425,88 @@ class DeviceSegmentReduce : public LuisaModule {
                                       d_out.data(), num_segments, d_begin_offsets.data(), d_end_offsets.data(),
                                       cmdlist.stream),
               "DeviceSegmentReduce::Sum");
+    }
+    template <class T>
+    void Sum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             uint num_segments, uint segment_size)
+    {
+        Reduce(cmdlist, temp_storage, d_in, d_out, num_segments, segment_size, SumOp{}, T(0));
+    }
+    template <class T>
+    void Min(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             uint num_segments, BufferView<uint> d_begin_offsets, BufferView<uint> d_end_offsets)
+    {
+        Reduce(cmdlist, temp_storage, d_in, d_out, num_segments, d_begin_offsets, d_end_offsets, MinOp{},
+               std::numeric_limits<T>::max());
+    }
+    template <class T>
+    void Min(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             uint num_segments, uint segment_size)
+    {
+        Reduce(cmdlist, temp_storage, d_in, d_out, num_segments, segment_size, MinOp{}, std::numeric_limits<T>::max());
+    }
+    template <class T>
+    void Max(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             uint num_segments, BufferView<uint> d_begin_offsets, BufferView<uint> d_end_offsets)
+    {
+        Reduce(cmdlist, temp_storage, d_in, d_out, num_segments, d_begin_offsets, d_end_offsets, MaxOp{},
+               std::numeric_limits<T>::lowest());
+    }
+    template <class T>
+    void Max(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             uint num_segments, uint segment_size)
+    {
+        Reduce(cmdlist, temp_storage, d_in, d_out, num_segments, segment_size, MaxOp{},
+               std::numeric_limits<T>::lowest());
+    }
+    /* device/device_segment_reduce.h:197-234 */
+    template <class T>
+    void ArgMax(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, uint num_segments, BufferView<uint> d_begin_offsets,
+                BufferView<uint> d_end_offsets)
+    {
+        check(lcpp_segment_reduce_argmax(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
+                                         d_out.data(), d_index_out.data(), num_segments, d_begin_offsets.data(),
+                                         d_end_offsets.data(), cmdlist.stream),
+              "DeviceSegmentReduce::ArgMax");
+    }
+    /* device/device_segment_reduce.h:236-272 */
+    template <class T>
+    void ArgMax(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, uint num_segments, uint segment_size)
+    {
+        check(lcpp_segment_reduce_argmax_fixed(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(),
+                                               d_in.data(), d_out.data(), d_index_out.data(), num_segments,
+                                               segment_size, cmdlist.stream),
+              "DeviceSegmentReduce::ArgMax");
+    }
+    /* device/device_segment_reduce.h:274-312 (the reference spells this overload Argmin) */
+    template <class T>
+    void ArgMin(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, uint num_segments, BufferView<uint> d_begin_offsets,
+                BufferView<uint> d_end_offsets)
+    {
+        check(lcpp_segment_reduce_argmin(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
+                                         d_out.data(), d_index_out.data(), num_segments, d_begin_offsets.data(),
+                                         d_end_offsets.data(), cmdlist.stream),
+              "DeviceSegmentReduce::ArgMin");
+    }
+    template <class T>
+    void Argmin(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, uint num_segments, BufferView<uint> d_begin_offsets,
+                BufferView<uint> d_end_offsets)
+    {
+        ArgMin(cmdlist, temp_storage, d_in, d_out, d_index_out, num_segments, d_begin_offsets, d_end_offsets);
+    }
+    /* device/device_segment_reduce.h:314-349 */
+    template <class T>
+    void ArgMin(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, uint num_segments, uint segment_size)
+    {
+        check(lcpp_segment_reduce_argmin_fixed(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(),
+                                               d_in.data(), d_out.data(), d_index_out.data(), num_segments,
+                                               segment_size, cmdlist.stream),
+              "DeviceSegmentReduce::ArgMin");
     }
 };
 

@@ -205,6 +205,41 @@ int lcpp_segment_reduce_temp_bytes(lcpp_dtype t, uint64_t num_segments, size_t *
 int lcpp_segment_reduce_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in,
                             void *out, uint64_t num_segments, const uint32_t *begin,
                             const uint32_t *end, void *stream);
+/* replaces DeviceSegmentReduce::Reduce(cmdlist, temp, d_in, d_out, num_segments, d_begin_offsets,
+ * d_end_offsets, reduce_op, initial_value), device_segment_reduce.h:94-107, and Min/Max
+ * (:144-195, init max() / lowest()): out[s] = op(init, op-fold of in[begin[s] .. end[s]));
+ * an empty segment gives init.  *init is a host value of type t (NULL: the op's identity). */
+int lcpp_segment_reduce(lcpp_dtype t, lcpp_reduce_op op, void *temp, size_t temp_bytes, const void *in,
+                        void *out, uint64_t num_segments, const uint32_t *begin, const uint32_t *end,
+                        const void *init, void *stream);
+/* replaces DeviceSegmentReduce::Reduce(cmdlist, temp, d_in, d_out, num_segments, segment_size,
+ * reduce_op, initial_value), device_segment_reduce.h:109-123 (and the fixed-size Sum/Min/Max):
+ * segment s = in[s * segment_size .. (s + 1) * segment_size).  num_segments * segment_size < 2^32. */
+int lcpp_segment_reduce_fixed(lcpp_dtype t, lcpp_reduce_op op, void *temp, size_t temp_bytes,
+                              const void *in, void *out, uint64_t num_segments, uint32_t segment_size,
+                              const void *init, void *stream);
+/* replaces DeviceSegmentReduce::GetArgTempStorageBytes<T>(num_item, num_segments),
+ * device_segment_reduce.h:77-89 (always 0 here) */
+int lcpp_segment_reduce_arg_temp_bytes(lcpp_dtype t, uint64_t n, uint64_t num_segments, size_t *bytes);
+/* replaces DeviceSegmentReduce::Argmin (CSR offsets), device_segment_reduce.h:274-312:
+ * out[s] = smallest value of the segment, index_out[s] = its index relative to begin[s] (ties:
+ * the smallest index); an empty segment gives (max(), 1) (the reference writes 1 - begin[s]). */
+int lcpp_segment_reduce_argmin(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                               uint32_t *index_out, uint64_t num_segments, const uint32_t *begin,
+                               const uint32_t *end, void *stream);
+/* replaces DeviceSegmentReduce::ArgMax (CSR offsets), device_segment_reduce.h:197-234: largest
+ * value, ties to the largest index; an empty segment gives (lowest(), 1). */
+int lcpp_segment_reduce_argmax(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                               uint32_t *index_out, uint64_t num_segments, const uint32_t *begin,
+                               const uint32_t *end, void *stream);
+/* replaces DeviceSegmentReduce::ArgMin(..., num_segments, segment_size), device_segment_reduce.h:314-349 */
+int lcpp_segment_reduce_argmin_fixed(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                                     uint32_t *index_out, uint64_t num_segments, uint32_t segment_size,
+                                     void *stream);
+/* replaces DeviceSegmentReduce::ArgMax(..., num_segments, segment_size), device_segment_reduce.h:236-272 */
+int lcpp_segment_reduce_argmax_fixed(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in, void *out,
+                                     uint32_t *index_out, uint64_t num_segments, uint32_t segment_size,
+                                     void *stream);
 
 /* ---------------------------------------------------------------------
  * Instrumentation (no counterpart in the reference).  When enabled, every

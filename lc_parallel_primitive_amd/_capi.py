@@ -54,6 +54,13 @@ SIGNATURES = {
     "lcpp_reduce_by_key": (_i, [_i, _i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp, _vp, _u64, _vp]),
     "lcpp_segment_reduce_temp_bytes": (_i, [_i, _u64, _c_size_p]),
     "lcpp_segment_reduce_sum": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp, _vp, _vp]),
+    "lcpp_segment_reduce": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp, _vp, _vp, _vp]),
+    "lcpp_segment_reduce_fixed": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _u64, ctypes.c_uint32, _vp, _vp]),
+    "lcpp_segment_reduce_arg_temp_bytes": (_i, [_i, _u64, _u64, _c_size_p]),
+    "lcpp_segment_reduce_argmin": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, _vp, _vp, _vp]),
+    "lcpp_segment_reduce_argmax": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, _vp, _vp, _vp]),
+    "lcpp_segment_reduce_argmin_fixed": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, ctypes.c_uint32, _vp]),
+    "lcpp_segment_reduce_argmax_fixed": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, ctypes.c_uint32, _vp]),
     "lcpp_profile_enable": (_i, [_i]),
     "lcpp_profile_count": (_i, []),
     "lcpp_profile_get": (_i, [_i, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double)]),

@@ -1,25 +1,39 @@
-// segment_reduce.hip — DeviceSegmentReduce::Sum with CSR begin/end offsets.
+// segment_reduce.hip — DeviceSegmentReduce::Reduce/Sum/Min/Max/ArgMin/ArgMax
+// over CSR begin/end offsets or fixed-size segments, for gfx950.
 //
-// Reference: device/device_segment_reduce.h:94-135, 353-381 and
-// device/details/segment_reduce.h:43-86: one 256-thread workgroup per
-// segment (2^20 workgroups at the benchmark size, most lanes idle for a mean
-// segment length of 128); no temp storage.
+// Reference: device/device_segment_reduce.h:94-349 (entry points), 353-431
+// (dispatch: one workgroup per segment, or for fixed-size segments of at
+// most small_items_per_tile a warp per segment), device/details/
+// segment_reduce.h:43-164 (kernels: out[s] = reduce_op(init, aggregate),
+// an empty segment writes init), segment_reduce.h:166-240 (Arg*: (index,
+// value) pairs over the whole input, then index - begin per segment).
 //
-// MI355X design, one launch, no temp storage, length-adaptive:
-//  * A workgroup (4 waves) owns a batch of 256 consecutive segments; thread t
-//    loads begin/end of segment t of the batch (coalesced).
-//  * Short segments (<= kSegLong elements): wave-per-segment.  Wave w walks
-//    its 64 segments 8 at a time: the bounds are read out of the lanes into
-//    scalar registers and each lane accumulates element (lane + 64c) of each
-//    of the 8 segments, two 64-element chunks per segment in flight (16
-//    independent loads per wave).  Each total is a 64-lane butterfly; lane l
-//    keeps the total of segment l and the wave stores its 64 results with
-//    one coalesced store.
-//  * Long segments: workgroup-per-segment.  Their indices are compacted into
+// MI355X design, one launch, no temp storage, segment-length adaptive:
+//  * A workgroup (4 waves) owns 256 consecutive segments, 64 per wave; lanes
+//    0..63 of a wave load the bounds of its segments with one coalesced load
+//    (or compute them, for fixed-size segments).
+//  * Wave-per-segment for segments up to kSegLong elements: the wave walks its
+//    64 segments 8 at a time; the 8 bounds are read out of the lanes into
+//    scalar registers and lane l accumulates elements l, l + 64, ... of each,
+//    two 64-element chunks per segment in flight (16 independent loads per
+//    lane); a 64-lane butterfly per segment leaves its result in the lane of
+//    that segment, and the wave stores its 64 results together.
+//  * Workgroup-per-segment for longer ones: their indices are compacted into
 //    LDS and the whole workgroup streams each one (4 loads in flight per
-//    thread), then folds the four wave totals.
-//  * An empty segment (end <= begin) gives exactly +0 (the reference writes
-//    its init value, 0).
+//    thread) after its waves are done.  Fixed-size segments longer than
+//    kSegLong take a workgroup-per-segment launch directly.
+//  * Sum/Min/Max write op(init, fold) (init defaults to the operator's
+//    identity; Min starts from max(), Max from lowest()); an empty segment
+//    (end <= begin, or segment_size 0) writes init.  Arg* keep
+//    (value, element index) pairs with the reference's tie rules (ArgMin:
+//    smaller value, then smaller index; ArgMax: larger value, then larger
+//    index, common/thread_operators.h:19-47) and report the index relative
+//    to the segment's first element; an empty segment gives index 1 and
+//    value max() (ArgMin) / lowest() (ArgMax).  The fold starts from the
+//    segment's own elements (no sentinel value takes part), so +-inf
+//    elements are found like any other.
+#include <cstring>
+
 #include "common.hpp"
 
 namespace lcpp {
@@ -27,117 +41,323 @@ namespace {
 
 constexpr int kSegBlock = 256;
 constexpr int kSegWaves = kSegBlock / kWave;
-constexpr int kSegUnroll = 8;
+// Segments in flight per wave and segments per wave.  Measured at C5
+// (2^27 f32, 2^20 segments of mean length 128, us): 4 / 8 / 16 in flight:
+// 128 / 118 / 142; 16 / 32 / 64 per wave: 121 / 119 / 117.  A persistent
+// grid of waves striding over groups of 8 measured 141-190 us, and 16-byte
+// vector loads with index masking 127 us (fewer waves fit).
+constexpr int kSegGroup = 8;
+constexpr int kSegPerWave = 64;
 constexpr uint32_t kSegLong = 8192;
+constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
+
+enum SegOpKind { kSegSum = 0, kSegMin = 1, kSegMax = 2, kSegArgMin = 3, kSegArgMax = 4 };
 
 template <class T>
-__global__ __launch_bounds__(kSegBlock) void segment_sum_kernel(const T *__restrict__ in,
-                                                                T *__restrict__ out,
-                                                                uint64_t num_segments,
-                                                                const uint32_t *__restrict__ begin,
-                                                                const uint32_t *__restrict__ end)
+struct SegPair {
+    T value;
+    uint32_t index;  // kNoIndex: no element folded yet
+};
+
+// Accumulator of one segment: T for Sum/Min/Max, SegPair<T> for Arg*.
+template <class T, int OP>
+struct SegAcc {
+    static constexpr bool kArg = OP >= kSegArgMin;
+    using A = std::conditional_t<kArg, SegPair<T>, T>;
+
+    static __host__ __device__ __forceinline__ A identity()
+    {
+        if constexpr (OP == kSegSum) return SumOp::identity<T>();
+        else if constexpr (OP == kSegMin) return MinOp::identity<T>();
+        else if constexpr (OP == kSegMax) return MaxOp::identity<T>();
+        else return A{T(0), kNoIndex};
+    }
+    static __device__ __forceinline__ A combine(A a, A b)
+    {
+        if constexpr (OP == kSegSum) return SumOp()(a, b);
+        else if constexpr (OP == kSegMin) return MinOp()(a, b);
+        else if constexpr (OP == kSegMax) return MaxOp()(a, b);
+        else {
+            if (b.index == kNoIndex) return a;
+            if (a.index == kNoIndex) return b;
+            const bool take = OP == kSegArgMax ? (b.value > a.value || (b.value == a.value && b.index > a.index))
+                                               : (b.value < a.value || (b.value == a.value && b.index < a.index));
+            return take ? b : a;
+        }
+    }
+    // fold element x at global index i
+    static __device__ __forceinline__ A fold(A a, T x, uint32_t i)
+    {
+        if constexpr (kArg) return combine(a, A{x, i});
+        else return combine(a, x);
+    }
+    static __device__ __forceinline__ A shfl_xor_acc(A a, int m)
+    {
+        if constexpr (kArg) {
+            A r;
+            r.value = shfl_xor(a.value, m);
+            r.index = (uint32_t)__shfl_xor((int)a.index, m);
+            return r;
+        } else {
+            return shfl_xor(a, m);
+        }
+    }
+    static __device__ __forceinline__ A wave_reduce(A a)
+    {
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) a = combine(a, shfl_xor_acc(a, m));
+        return a;
+    }
+};
+
+// Where the segments come from: CSR begin/end arrays or fixed-size runs.
+struct SegBounds {
+    const uint32_t *begin, *end;  // CSR (null for fixed-size)
+    uint32_t size;                // fixed-size segment length
+};
+
+template <bool FIXED>
+__device__ __forceinline__ void seg_bounds(const SegBounds &sb, uint64_t s, uint64_t S, uint32_t &b, uint32_t &len)
 {
-    __shared__ uint32_t s_long[kSegBlock];
-    __shared__ uint32_t s_nlong;
-    __shared__ T s_wave[kSegWaves];
-    SumOp op;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lane = lane_id();
-    const uint32_t wave = tid / kWave;
-    const uint64_t batch0 = (uint64_t)blockIdx.x * kSegBlock;
-    const uint64_t my_seg = batch0 + tid;
-
-    uint32_t b = 0, len = 0;
-    if (my_seg < num_segments) {
-        b = begin[my_seg];
-        const uint32_t e = end[my_seg];
-        len = e > b ? e - b : 0;
-    }
-    if (tid == 0) s_nlong = 0;
-    __syncthreads();
-    const bool is_long = len > kSegLong;
-    if (is_long) s_long[atomicAdd(&s_nlong, 1u)] = tid;
-    if (is_long) len = 0;  // summed by the whole workgroup below
-
-    // ---- short segments: wave per segment
-    T mine = T(0);
-#pragma unroll 1
-    for (int j0 = 0; j0 < kWave; j0 += kSegUnroll) {
-        uint32_t bj[kSegUnroll], lj[kSegUnroll];
-        uint32_t maxlen = 0;
-#pragma unroll
-        for (int u = 0; u < kSegUnroll; ++u) {
-            bj[u] = __builtin_amdgcn_readlane(b, j0 + u);
-            lj[u] = __builtin_amdgcn_readlane(len, j0 + u);
-            maxlen = lj[u] > maxlen ? lj[u] : maxlen;
+    b = 0;
+    len = 0;
+    if (s < S) {
+        if constexpr (FIXED) {
+            b = (uint32_t)s * sb.size;
+            len = sb.size;
+        } else {
+            b = sb.begin[s];
+            const uint32_t e = sb.end[s];
+            len = e > b ? e - b : 0;
         }
-        if (maxlen == 0) continue;
-        T acc[kSegUnroll];
-#pragma unroll
-        for (int u = 0; u < kSegUnroll; ++u) acc[u] = T(0);
-#pragma unroll 1
-        for (uint32_t c = lane; c < maxlen; c += 2 * kWave) {
-            T x0[kSegUnroll], x1[kSegUnroll];
-#pragma unroll
-            for (int u = 0; u < kSegUnroll; ++u) {
-                x0[u] = c < lj[u] ? in[(uint64_t)bj[u] + c] : T(0);
-                x1[u] = c + kWave < lj[u] ? in[(uint64_t)bj[u] + c + kWave] : T(0);
-            }
-#pragma unroll
-            for (int u = 0; u < kSegUnroll; ++u) acc[u] = op(op(acc[u], x0[u]), x1[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < kSegUnroll; ++u) {
-            if (lj[u] == 0) continue;
-            const T r = wave_allreduce(acc[u], op);
-            if (lane == (uint32_t)(j0 + u)) mine = r;
-        }
-    }
-    if (my_seg < num_segments && !is_long) out[my_seg] = mine;
-
-    // ---- long segments: workgroup per segment
-    __syncthreads();
-    const uint32_t nlong = s_nlong;
-    for (uint32_t q = 0; q < nlong; ++q) {
-        const uint64_t s = batch0 + s_long[q];
-        const uint64_t lb = begin[s], le = end[s];
-        T acc0 = T(0), acc1 = T(0), acc2 = T(0), acc3 = T(0);
-        uint64_t i = lb + tid;
-        for (; i + 3 * kSegBlock < le; i += 4 * kSegBlock) {
-            acc0 = op(acc0, in[i]);
-            acc1 = op(acc1, in[i + kSegBlock]);
-            acc2 = op(acc2, in[i + 2 * kSegBlock]);
-            acc3 = op(acc3, in[i + 3 * kSegBlock]);
-        }
-        for (; i < le; i += kSegBlock) acc0 = op(acc0, in[i]);
-        T acc = op(op(acc0, acc1), op(acc2, acc3));
-        acc = wave_allreduce(acc, op);
-        if (lane == 0) s_wave[wave] = acc;
-        __syncthreads();
-        if (tid == 0) {
-            T r = s_wave[0];
-#pragma unroll
-            for (int w = 1; w < kSegWaves; ++w) r = op(r, s_wave[w]);
-            out[s] = r;
-        }
-        __syncthreads();
     }
 }
 
-template <class T>
-int segment_launch(const void *in_, void *out_, uint64_t S, const uint32_t *begin,
-                   const uint32_t *end, hipStream_t s)
+// Result of one segment: out[s] (+ index_out[s] for Arg*).
+template <class T, int OP>
+__device__ __forceinline__ void seg_store(typename SegAcc<T, OP>::A acc, uint32_t b, T init, T *out,
+                                          uint32_t *index_out, uint64_t s)
+{
+    using Acc = SegAcc<T, OP>;
+    if constexpr (Acc::kArg) {
+        const bool empty = acc.index == kNoIndex;
+        out[s] = empty ? (OP == kSegArgMax ? std::numeric_limits<T>::lowest() : std::numeric_limits<T>::max())
+                       : acc.value;
+        index_out[s] = empty ? 1u : acc.index - b;
+    } else {
+        out[s] = Acc::combine(init, acc);
+    }
+}
+
+// The whole workgroup streams segment s (4 loads in flight per thread) and
+// thread 0 stores its result.  Every thread must call it (barriers).
+template <class T, int OP, bool FIXED>
+__device__ __forceinline__ void wg_reduce_segment(const T *__restrict__ in, T *__restrict__ out,
+                                                  uint32_t *__restrict__ index_out, uint64_t s, uint64_t S,
+                                                  const SegBounds &sb, T init,
+                                                  typename SegAcc<T, OP>::A (&s_wave)[kSegWaves])
+{
+    using Acc = SegAcc<T, OP>;
+    using A = typename Acc::A;
+    const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    uint32_t lb, llen;
+    seg_bounds<FIXED>(sb, s, S, lb, llen);
+    const uint64_t le = (uint64_t)lb + llen;
+    A a0 = Acc::identity(), a1 = a0, a2 = a0, a3 = a0;
+    uint64_t i = (uint64_t)lb + tid;
+    for (; i + 3 * kSegBlock < le; i += 4 * kSegBlock) {
+        const T x0 = in[i], x1 = in[i + kSegBlock], x2 = in[i + 2 * kSegBlock], x3 = in[i + 3 * kSegBlock];
+        a0 = Acc::fold(a0, x0, (uint32_t)i);
+        a1 = Acc::fold(a1, x1, (uint32_t)(i + kSegBlock));
+        a2 = Acc::fold(a2, x2, (uint32_t)(i + 2 * kSegBlock));
+        a3 = Acc::fold(a3, x3, (uint32_t)(i + 3 * kSegBlock));
+    }
+    for (; i < le; i += kSegBlock) a0 = Acc::fold(a0, in[i], (uint32_t)i);
+    A a = Acc::combine(Acc::combine(a0, a1), Acc::combine(a2, a3));
+    a = Acc::wave_reduce(a);
+    if (lane == 0) s_wave[wave] = a;
+    __syncthreads();
+    if (tid == 0) {
+        A r = s_wave[0];
+#pragma unroll
+        for (int w = 1; w < kSegWaves; ++w) r = Acc::combine(r, s_wave[w]);
+        seg_store<T, OP>(r, lb, init, out, index_out, s);
+    }
+    __syncthreads();
+}
+
+template <class T, int OP, bool FIXED>
+__global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__restrict__ in, T *__restrict__ out,
+                                                                   uint32_t *__restrict__ index_out, uint64_t S,
+                                                                   SegBounds sb, T init)
+{
+    using Acc = SegAcc<T, OP>;
+    using A = typename Acc::A;
+    constexpr int kBatch = kSegWaves * kSegPerWave;
+    __shared__ uint32_t s_long[kBatch];
+    __shared__ uint32_t s_nlong;
+    __shared__ A s_wave[kSegWaves];
+
+    const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const uint64_t wseg0 = (uint64_t)blockIdx.x * kBatch + (uint64_t)wave * kSegPerWave;
+    // lanes 0..kSegPerWave-1 hold the bounds of the wave's segments (one coalesced load)
+    uint32_t b = 0, len = 0;
+    if (lane < (uint32_t)kSegPerWave) seg_bounds<FIXED>(sb, wseg0 + lane, S, b, len);
+    if (tid == 0) s_nlong = 0;
+    __syncthreads();
+    const bool is_long = len > kSegLong;
+    if (is_long) s_long[atomicAdd(&s_nlong, 1u)] = (uint32_t)(wave * kSegPerWave + lane);
+
+    A mine = Acc::identity();
+#pragma unroll 1
+    for (int j0 = 0; j0 < kSegPerWave; j0 += kSegGroup) {
+        uint32_t bj[kSegGroup], lj[kSegGroup];
+        uint32_t maxlen = 0;
+#pragma unroll
+        for (int u = 0; u < kSegGroup; ++u) {
+            bj[u] = __builtin_amdgcn_readlane(b, j0 + u);
+            const uint32_t l = __builtin_amdgcn_readlane(len, j0 + u);
+            lj[u] = l > kSegLong ? 0u : l;  // long segments: workgroup path below
+            maxlen = lj[u] > maxlen ? lj[u] : maxlen;
+        }
+        if (maxlen == 0) continue;
+        A acc[kSegGroup];
+#pragma unroll
+        for (int u = 0; u < kSegGroup; ++u) acc[u] = Acc::identity();
+#pragma unroll 1
+            for (uint32_t c = lane; c < maxlen; c += 2 * kWave) {
+                T x0[kSegGroup], x1[kSegGroup];
+#pragma unroll
+                for (int u = 0; u < kSegGroup; ++u) {
+                    x0[u] = c < lj[u] ? in[(uint64_t)bj[u] + c] : T(0);
+                    x1[u] = c + kWave < lj[u] ? in[(uint64_t)bj[u] + c + kWave] : T(0);
+                }
+#pragma unroll
+                for (int u = 0; u < kSegGroup; ++u) {
+                    if constexpr (OP == kSegSum) {
+                        acc[u] = Acc::fold(Acc::fold(acc[u], x0[u], 0), x1[u], 0);  // out-of-range loads are 0
+                    } else {
+                        if (c < lj[u]) acc[u] = Acc::fold(acc[u], x0[u], bj[u] + c);
+                        if (c + kWave < lj[u]) acc[u] = Acc::fold(acc[u], x1[u], bj[u] + c + kWave);
+                    }
+                }
+            }
+#pragma unroll
+        for (int u = 0; u < kSegGroup; ++u) {
+            if (lj[u] == 0) continue;
+            const A r = Acc::wave_reduce(acc[u]);
+            if (lane == (uint32_t)(j0 + u)) mine = r;
+        }
+    }
+    if (lane < (uint32_t)kSegPerWave && wseg0 + lane < S && !is_long)
+        seg_store<T, OP>(mine, b, init, out, index_out, wseg0 + lane);
+
+    // ---- long segments: the whole workgroup streams each one
+    __syncthreads();
+    const uint32_t nlong = s_nlong;
+    for (uint32_t q = 0; q < nlong; ++q)
+        wg_reduce_segment<T, OP, FIXED>(in, out, index_out, (uint64_t)blockIdx.x * kBatch + s_long[q], S, sb, init,
+                                        s_wave);
+}
+
+// Fixed-size segments longer than kSegLong: one workgroup per segment.
+template <class T, int OP>
+__global__ __launch_bounds__(kSegBlock) void segment_reduce_wg_kernel(const T *__restrict__ in, T *__restrict__ out,
+                                                                      uint32_t *__restrict__ index_out, uint64_t S,
+                                                                      SegBounds sb, T init)
+{
+    __shared__ typename SegAcc<T, OP>::A s_wave[kSegWaves];
+    for (uint64_t s = blockIdx.x; s < S; s += gridDim.x) wg_reduce_segment<T, OP, true>(in, out, index_out, s, S, sb, init, s_wave);
+}
+
+int num_cus_cached()
+{
+    static int cached = 0;
+    if (!cached) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            cached = cus;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
+// Workgroups of `kernel` the device holds at once (cached per kernel).
+template <class K>
+int resident_blocks(K kernel, int &cache)
+{
+    if (!cache) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kernel), kSegBlock, 0) !=
+                hipSuccess ||
+            per_cu <= 0)
+            per_cu = 4;
+        cache = per_cu * num_cus_cached();
+    }
+    return cache;
+}
+
+template <class T, int OP, bool FIXED>
+int segment_launch(const void *in_, void *out_, uint32_t *index_out, uint64_t S, SegBounds sb, const void *init_,
+                   hipStream_t s)
 {
     if (S == 0) return LCPP_OK;
     const T *in = static_cast<const T *>(in_);
     T *out = static_cast<T *>(out_);
-    if (!out || !begin || !end) return LCPP_ERR_INVALID_ARG;
-    const uint64_t blocks = ceil_div(S, kSegBlock);
-    if (blocks > 0x7FFFFFFFull) return LCPP_ERR_INVALID_ARG;
-    LCPP_LAUNCH("segment_sum", s,
-                segment_sum_kernel<T><<<(uint32_t)blocks, kSegBlock, 0, s>>>(in, out, S, begin, end));
+    if (!out || (OP >= kSegArgMin && !index_out)) return LCPP_ERR_INVALID_ARG;
+    if (!FIXED && (!sb.begin || !sb.end || !in)) return LCPP_ERR_INVALID_ARG;
+    if (FIXED && sb.size && !in) return LCPP_ERR_INVALID_ARG;
+    if (S > 0xFFFFFFFFull || ceil_div(S, (uint64_t)kSegWaves * kSegPerWave) > 0x7FFFFFFFull) return LCPP_ERR_INVALID_ARG;
+    if (FIXED && (uint64_t)sb.size * S > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;  // 32-bit element offsets
+    T init = SegAcc<T, OP >= kSegArgMin ? kSegSum : OP>::identity();
+    if constexpr (OP < kSegArgMin) {
+        if (init_) memcpy(&init, init_, sizeof(T));
+    }
+    if (FIXED && sb.size > kSegLong) {
+        static int cap = 0;
+        const uint64_t c = (uint64_t)resident_blocks(&segment_reduce_wg_kernel<T, OP>, cap);
+        const uint32_t grid = (uint32_t)(S < c ? S : c);
+        LCPP_LAUNCH("segment_reduce_wg", s,
+                    (segment_reduce_wg_kernel<T, OP><<<grid, kSegBlock, 0, s>>>(in, out, index_out, S, sb, init)));
+        LCPP_CHECK_LAUNCH();
+        return LCPP_OK;
+    }
+    const uint64_t blocks = ceil_div(S, (uint64_t)kSegWaves * kSegPerWave);
+    const uint32_t grid = (uint32_t)blocks;
+    LCPP_LAUNCH("segment_reduce", s,
+                (segment_reduce_kernel<T, OP, FIXED><<<grid, kSegBlock, 0, s>>>(in, out, index_out, S, sb, init)));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
+}
+
+template <int OP, bool FIXED>
+int segment_dispatch(lcpp_dtype t, const void *in, void *out, uint32_t *index_out, uint64_t S, SegBounds sb,
+                     const void *init, void *stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (t) {
+    case LCPP_INT32: return segment_launch<int32_t, OP, FIXED>(in, out, index_out, S, sb, init, s);
+    case LCPP_UINT32: return segment_launch<uint32_t, OP, FIXED>(in, out, index_out, S, sb, init, s);
+    case LCPP_FLOAT32: return segment_launch<float, OP, FIXED>(in, out, index_out, S, sb, init, s);
+    case LCPP_INT64: return segment_launch<int64_t, OP, FIXED>(in, out, index_out, S, sb, init, s);
+    case LCPP_UINT64: return segment_launch<uint64_t, OP, FIXED>(in, out, index_out, S, sb, init, s);
+    case LCPP_FLOAT64: return segment_launch<double, OP, FIXED>(in, out, index_out, S, sb, init, s);
+    default: return LCPP_ERR_UNSUPPORTED_DTYPE;
+    }
+}
+
+template <bool FIXED>
+int segment_op_dispatch(lcpp_dtype t, lcpp_reduce_op op, const void *in, void *out, uint64_t S, SegBounds sb,
+                        const void *init, void *stream)
+{
+    switch (op) {
+    case LCPP_OP_SUM: return segment_dispatch<kSegSum, FIXED>(t, in, out, nullptr, S, sb, init, stream);
+    case LCPP_OP_MIN: return segment_dispatch<kSegMin, FIXED>(t, in, out, nullptr, S, sb, init, stream);
+    case LCPP_OP_MAX: return segment_dispatch<kSegMax, FIXED>(t, in, out, nullptr, S, sb, init, stream);
+    default: return LCPP_ERR_INVALID_ARG;
+    }
 }
 
 }  // namespace
@@ -153,18 +373,56 @@ extern "C" int lcpp_segment_reduce_temp_bytes(lcpp_dtype t, uint64_t, size_t *by
     return LCPP_OK;
 }
 
-extern "C" int lcpp_segment_reduce_sum(lcpp_dtype t, void *, size_t, const void *in, void *out,
-                                       uint64_t S, const uint32_t *begin, const uint32_t *end,
-                                       void *stream)
+extern "C" int lcpp_segment_reduce_arg_temp_bytes(lcpp_dtype t, uint64_t, uint64_t, size_t *bytes)
 {
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    switch (t) {
-    case LCPP_INT32: return segment_launch<int32_t>(in, out, S, begin, end, s);
-    case LCPP_UINT32: return segment_launch<uint32_t>(in, out, S, begin, end, s);
-    case LCPP_FLOAT32: return segment_launch<float>(in, out, S, begin, end, s);
-    case LCPP_INT64: return segment_launch<int64_t>(in, out, S, begin, end, s);
-    case LCPP_UINT64: return segment_launch<uint64_t>(in, out, S, begin, end, s);
-    case LCPP_FLOAT64: return segment_launch<double>(in, out, S, begin, end, s);
-    default: return LCPP_ERR_UNSUPPORTED_DTYPE;
-    }
+    return lcpp_segment_reduce_temp_bytes(t, 0, bytes);
+}
+
+extern "C" int lcpp_segment_reduce_sum(lcpp_dtype t, void *, size_t, const void *in, void *out, uint64_t S,
+                                       const uint32_t *begin, const uint32_t *end, void *stream)
+{
+    return segment_op_dispatch<false>(t, LCPP_OP_SUM, in, out, S, SegBounds{begin, end, 0}, nullptr, stream);
+}
+
+extern "C" int lcpp_segment_reduce(lcpp_dtype t, lcpp_reduce_op op, void *, size_t, const void *in, void *out,
+                                   uint64_t S, const uint32_t *begin, const uint32_t *end, const void *init,
+                                   void *stream)
+{
+    return segment_op_dispatch<false>(t, op, in, out, S, SegBounds{begin, end, 0}, init, stream);
+}
+
+extern "C" int lcpp_segment_reduce_fixed(lcpp_dtype t, lcpp_reduce_op op, void *, size_t, const void *in, void *out,
+                                         uint64_t S, uint32_t segment_size, const void *init, void *stream)
+{
+    return segment_op_dispatch<true>(t, op, in, out, S, SegBounds{nullptr, nullptr, segment_size}, init, stream);
+}
+
+extern "C" int lcpp_segment_reduce_argmin(lcpp_dtype t, void *, size_t, const void *in, void *out,
+                                          uint32_t *index_out, uint64_t S, const uint32_t *begin,
+                                          const uint32_t *end, void *stream)
+{
+    return segment_dispatch<kSegArgMin, false>(t, in, out, index_out, S, SegBounds{begin, end, 0}, nullptr, stream);
+}
+
+extern "C" int lcpp_segment_reduce_argmax(lcpp_dtype t, void *, size_t, const void *in, void *out,
+                                          uint32_t *index_out, uint64_t S, const uint32_t *begin,
+                                          const uint32_t *end, void *stream)
+{
+    return segment_dispatch<kSegArgMax, false>(t, in, out, index_out, S, SegBounds{begin, end, 0}, nullptr, stream);
+}
+
+extern "C" int lcpp_segment_reduce_argmin_fixed(lcpp_dtype t, void *, size_t, const void *in, void *out,
+                                                uint32_t *index_out, uint64_t S, uint32_t segment_size,
+                                                void *stream)
+{
+    return segment_dispatch<kSegArgMin, true>(t, in, out, index_out, S, SegBounds{nullptr, nullptr, segment_size},
+                                              nullptr, stream);
+}
+
+extern "C" int lcpp_segment_reduce_argmax_fixed(lcpp_dtype t, void *, size_t, const void *in, void *out,
+                                                uint32_t *index_out, uint64_t S, uint32_t segment_size,
+                                                void *stream)
+{
+    return segment_dispatch<kSegArgMax, true>(t, in, out, index_out, S, SegBounds{nullptr, nullptr, segment_size},
+                                              nullptr, stream);
 }

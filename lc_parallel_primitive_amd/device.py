@@ -289,7 +289,9 @@ class DeviceRadixSort:
 
 
 class DeviceSegmentReduce:
-    """device/device_segment_reduce.h:26-135 (Sum with CSR begin/end offsets)."""
+    """device/device_segment_reduce.h:26-349: Reduce / Sum / Min / Max / ArgMin / ArgMax over CSR
+    begin/end offsets or over fixed-size segments (pass segment_size, an int, in place of the two
+    offset buffers, as the reference's overloads do)."""
 
     def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
         self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
@@ -298,25 +300,116 @@ class DeviceSegmentReduce:
         return self
 
     @staticmethod
-    def GetTempStorageBytes(dtype, num_segments: int = 0) -> int:
-        return _query(lib().lcpp_segment_reduce_temp_bytes, dtype_code(dtype), num_segments)
+    def GetTempStorageBytes(dtype, num_item: int = 0) -> int:
+        return _query(lib().lcpp_segment_reduce_temp_bytes, dtype_code(dtype), num_item)
 
-    def Sum(self, temp_storage, d_in, d_out, num_segments: int, d_begin_offsets, d_end_offsets, stream=None):
-        _need(d_out, num_segments, "d_out")
+    @staticmethod
+    def GetArgTempStorageBytes(dtype, num_item: int, num_segments: int) -> int:
+        """device_segment_reduce.h:77-89 (0 here: no key-value staging)"""
+        return _query(lib().lcpp_segment_reduce_arg_temp_bytes, dtype_code(dtype), num_item, num_segments)
+
+    @staticmethod
+    def _check_ranges(d_in, num_segments, offsets):
+        """Every segment must lie inside d_in (checked on the host: bad offsets
+        raise instead of faulting the GPU)."""
+        if not num_segments:
+            return
+        if isinstance(offsets[0], int):
+            size = offsets[0]
+            if size < 0 or num_segments * size > d_in.numel():
+                raise ValueError(f"{num_segments} segments of {size} exceed d_in ({d_in.numel()} elements)")
+            if num_segments * size >= 1 << 32:
+                raise ValueError("fixed-size segments must address fewer than 2^32 elements")
+            return
+        import torch
+
+        d_begin_offsets, d_end_offsets = offsets
         _need(d_begin_offsets, num_segments, "d_begin_offsets")
         _need(d_end_offsets, num_segments, "d_end_offsets")
-        _same_dtype(d_in, d_out, "Sum")
-        if num_segments:
-            import torch
+        b = d_begin_offsets[:num_segments].to(torch.int64)
+        e = d_end_offsets[:num_segments].to(torch.int64)
+        hi = torch.where(e > b, e, torch.zeros_like(e)).max().item()
+        if hi > d_in.numel():
+            raise ValueError(f"segment end {hi} exceeds d_in ({d_in.numel()} elements)")
 
-            # every segment must lie inside d_in (checked on the host, no GPU fault on bad offsets)
-            b = d_begin_offsets[:num_segments].to(torch.int64)
-            e = d_end_offsets[:num_segments].to(torch.int64)
-            hi = torch.where(e > b, e, torch.zeros_like(e)).max().item()
-            if hi > d_in.numel():
-                raise ValueError(f"segment end {hi} exceeds d_in ({d_in.numel()} elements)")
+    def _reduce(self, temp_storage, d_in, d_out, num_segments, offsets, op, init, stream, name):
+        _need(d_out, num_segments, "d_out")
+        _same_dtype(d_in, d_out, name)
+        if op not in LCPP_OPS:
+            raise ValueError(f"{name}: unsupported reduce_op {op!r}")
+        self._check_ranges(d_in, num_segments, offsets)
+        code = dtype_code(d_in.dtype)
+        iv = _host_value(code, init) if init is not None else None
+        ip = ctypes.c_void_p(iv.ctypes.data) if iv is not None else ctypes.c_void_p(0)
         L = lib()
-        check(L.lcpp_segment_reduce_sum(dtype_code(d_in.dtype), _ptr(temp_storage), _nbytes(temp_storage),
-                                        _ptr(d_in), _ptr(d_out), num_segments, _ptr(d_begin_offsets),
-                                        _ptr(d_end_offsets), _stream(stream)),
-              "lcpp_segment_reduce_sum")
+        if isinstance(offsets[0], int):
+            check(L.lcpp_segment_reduce_fixed(code, LCPP_OPS[op], _ptr(temp_storage), _nbytes(temp_storage),
+                                              _ptr(d_in), _ptr(d_out), num_segments, offsets[0], ip, _stream(stream)),
+                  "lcpp_segment_reduce_fixed")
+        else:
+            check(L.lcpp_segment_reduce(code, LCPP_OPS[op], _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in),
+                                        _ptr(d_out), num_segments, _ptr(offsets[0]), _ptr(offsets[1]), ip,
+                                        _stream(stream)),
+                  "lcpp_segment_reduce")
+
+    def Reduce(self, temp_storage, d_in, d_out, num_segments: int, *args, stream=None):
+        """Reduce(temp, d_in, d_out, num_segments, d_begin_offsets, d_end_offsets, reduce_op, initial_value)
+        or Reduce(temp, d_in, d_out, num_segments, segment_size, reduce_op, initial_value)
+        (device_segment_reduce.h:94-123): d_out[s] = reduce_op(initial_value, fold of segment s).
+        reduce_op: "sum" | "min" | "max"."""
+        if isinstance(args[0], int):
+            size, op, init = args
+            offsets = (size,)
+        else:
+            b, e, op, init = args
+            offsets = (b, e)
+        self._reduce(temp_storage, d_in, d_out, num_segments, offsets, op, init, stream, "Reduce")
+
+    @staticmethod
+    def _offsets(args):
+        return (args[0],) if isinstance(args[0], int) else (args[0], args[1])
+
+    def Sum(self, temp_storage, d_in, d_out, num_segments: int, *offsets, stream=None):
+        """device_segment_reduce.h:125-142 (CSR offsets, or a fixed segment_size)"""
+        self._reduce(temp_storage, d_in, d_out, num_segments, self._offsets(offsets), "sum", None, stream, "Sum")
+
+    def Min(self, temp_storage, d_in, d_out, num_segments: int, *offsets, stream=None):
+        """device_segment_reduce.h:144-168 (init numeric max)"""
+        self._reduce(temp_storage, d_in, d_out, num_segments, self._offsets(offsets), "min", None, stream, "Min")
+
+    def Max(self, temp_storage, d_in, d_out, num_segments: int, *offsets, stream=None):
+        """device_segment_reduce.h:170-195 (init numeric lowest)"""
+        self._reduce(temp_storage, d_in, d_out, num_segments, self._offsets(offsets), "max", None, stream, "Max")
+
+    def _arg(self, is_max, temp_storage, d_in, d_out, d_index_out, num_segments, offsets, stream):
+        name = "ArgMax" if is_max else "ArgMin"
+        _need(d_out, num_segments, "d_out")
+        _need(d_index_out, num_segments, "d_index_out")
+        _same_dtype(d_in, d_out, name)
+        if d_index_out.element_size() != 4:
+            raise TypeError(f"{name}: d_index_out must hold 32-bit indices")
+        offsets = self._offsets(offsets)
+        self._check_ranges(d_in, num_segments, offsets)
+        L = lib()
+        code = dtype_code(d_in.dtype)
+        if isinstance(offsets[0], int):
+            fn = L.lcpp_segment_reduce_argmax_fixed if is_max else L.lcpp_segment_reduce_argmin_fixed
+            check(fn(code, _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
+                     num_segments, offsets[0], _stream(stream)), fn.__name__)
+        else:
+            fn = L.lcpp_segment_reduce_argmax if is_max else L.lcpp_segment_reduce_argmin
+            check(fn(code, _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
+                     num_segments, _ptr(offsets[0]), _ptr(offsets[1]), _stream(stream)), fn.__name__)
+
+    def ArgMax(self, temp_storage, d_in, d_out, d_index_out, num_segments: int, *offsets, stream=None):
+        """device_segment_reduce.h:197-272: the largest value and its index within the segment
+        (ties: the largest index); an empty segment gives (lowest, 1)."""
+        self._arg(True, temp_storage, d_in, d_out, d_index_out, num_segments, offsets, stream)
+
+    def ArgMin(self, temp_storage, d_in, d_out, d_index_out, num_segments: int, *offsets, stream=None):
+        """device_segment_reduce.h:274-349: the smallest value and its index within the segment
+        (ties: the smallest index); an empty segment gives (max, 1)."""
+        self._arg(False, temp_storage, d_in, d_out, d_index_out, num_segments, offsets, stream)
+
+    # the reference spells the CSR overload Argmin (device_segment_reduce.h:275)
+    Argmin = ArgMin

@@ -836,10 +836,10 @@ int lcor_check_sorted_permutation_u32(const uint32_t *keys_in, const uint32_t *k
  * out[s] = init op reduce(in[begin[s] .. end[s])), empty -> init (+0).
  * ====================================================================== */
 int lcor_segment_reduce(int op, int dtype, const void *in, void *out, uint64_t num_segments,
-                        const uint32_t *begin, const uint32_t *end)
+                        const uint32_t *begin, const uint32_t *end, const void *init)
 {
     size_t es = dtype_size(dtype);
-    if (!es) return -1;
+    if (!es || op < 0 || op > 2) return -1;
     for (uint64_t s = 0; s < num_segments; ++s) {
         char *o = (char *)out + s * es;
         uint64_t acc = 0;
@@ -854,7 +854,64 @@ int lcor_segment_reduce(int op, int dtype, const void *in, void *out, uint64_t n
                 fold_any(op, dtype, (const char *)in + (size_t)begin[s] * es, end[s] - begin[s], &acc);
             }
         }
+        if (init) {  /* out = op(init, aggregate) (segment_reduce.h:81) */
+            uint64_t r = 0;
+            memcpy(&r, init, es);
+            fold_any(op, dtype, &acc, 1, &r);
+            acc = r;
+        }
         memcpy(o, &acc, es);
+    }
+    return 0;
+}
+
+/* Segment ArgMin / ArgMax — device/device_segment_reduce.h:197-349 and
+ * details/segment_reduce.h:166-240: (index, value) pairs folded with
+ * ArgMinOp / ArgMaxOp (common/thread_operators.h:19-47: ArgMin keeps the
+ * smaller value, on ties the smaller index; ArgMax the larger value, on ties
+ * the larger index), the index reported relative to begin[s].  An empty
+ * segment gives index 1 and value max() (ArgMin) / lowest() (ArgMax); the
+ * reference's arg_assign computes 1 - begin[s] there (segment_reduce.h
+ * :214-216), which wraps for begin > 1. */
+/* the first element of a non-empty segment starts the fold (no sentinel
+ * value takes part, so +-inf elements are found like any other) */
+#define SEG_ARG_FOLD(T)                                                                \
+    do {                                                                               \
+        const T *a = (const T *)in;                                                    \
+        if (e > b) {                                                                   \
+            T best = a[b];                                                             \
+            uint32_t bi = b;                                                           \
+            for (uint32_t i = b + 1; i < e; ++i) {                                     \
+                const T x = a[i];                                                      \
+                const int take = is_max ? (x > best || (x == best && i > bi))          \
+                                        : (x < best || (x == best && i < bi));         \
+                if (take) { best = x; bi = i; }                                        \
+            }                                                                          \
+            memcpy(&v, &best, sizeof(T));                                              \
+            idx = bi - b;                                                              \
+        }                                                                              \
+    } while (0)
+
+int lcor_segment_reduce_arg(int is_max, int dtype, const void *in, void *out, uint32_t *index_out,
+                            uint64_t num_segments, const uint32_t *begin, const uint32_t *end)
+{
+    const size_t es = dtype_size(dtype);
+    if (!es) return -1;
+    for (uint64_t s = 0; s < num_segments; ++s) {
+        uint64_t v = 0;
+        init_value(is_max ? LCOR_OP_MAX : LCOR_OP_MIN, dtype, &v);
+        uint32_t idx = 1;
+        const uint32_t b = begin[s], e = end[s];
+        switch (dtype) {
+        case LCOR_I32: SEG_ARG_FOLD(int32_t); break;
+        case LCOR_U32: SEG_ARG_FOLD(uint32_t); break;
+        case LCOR_F32: SEG_ARG_FOLD(float); break;
+        case LCOR_I64: SEG_ARG_FOLD(int64_t); break;
+        case LCOR_U64: SEG_ARG_FOLD(uint64_t); break;
+        case LCOR_F64: SEG_ARG_FOLD(double); break;
+        }
+        memcpy((char *)out + s * es, &v, es);
+        index_out[s] = idx;
     }
     return 0;
 }

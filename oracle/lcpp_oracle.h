@@ -29,8 +29,11 @@
  *   radix sort      numpy stable argsort/sort, reversed-keys KAT, float KAT
  *                   (libstdc++ mt19937 inputs, std::sort golden), stability
  *                   checker (planted-mistake tests)
- *   segment reduce  numpy per-segment sums, reference KAT (1024 shuffled ints,
- *                   segments of 100, std::accumulate golden)
+ *   segment reduce  numpy per-segment sums / min / max (with init), numpy
+ *                   argmin / reversed argmax per segment, reference KATs
+ *                   (1024 shuffled ints in segments of 100: sums and ArgMax;
+ *                   0..1023 in fixed segments of 32: sums; shuffled, fixed 32:
+ *                   ArgMin)
  *   scan by key     numpy cumsum differences inside runs (wraparound), single
  *                   run == plain scan, all-distinct keys == init / op(x, init),
  *                   reference KAT (keys i/100, ones -> i % 100)
@@ -113,8 +116,13 @@ int lcor_reduce_by_key_f64(int key_dtype, int val_dtype, const void *keys, const
                            uint64_t n, double *sums, double *abs_sums, uint64_t *num_runs);
 
 /* ---------------- segment reduce -------------------------------------- */
+/* out[s] = op(init, fold(in[begin[s] .. end[s]))); init NULL means the op's identity */
 int lcor_segment_reduce(int op, int dtype, const void *in, void *out, uint64_t num_segments,
-                        const uint32_t *begin, const uint32_t *end);
+                        const uint32_t *begin, const uint32_t *end, const void *init);
+/* ArgMin (is_max 0) / ArgMax (is_max 1) per segment, index relative to begin[s];
+ * an empty segment gives (1, max()) / (1, lowest()) */
+int lcor_segment_reduce_arg(int is_max, int dtype, const void *in, void *out, uint32_t *index_out,
+                            uint64_t num_segments, const uint32_t *begin, const uint32_t *end);
 int lcor_segment_reduce_f64(int dtype, const void *in, uint64_t num_segments,
                             const uint32_t *begin, const uint32_t *end, double *sum,
                             double *abs_sum);

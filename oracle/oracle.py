@@ -67,7 +67,8 @@ def lib() -> ctypes.CDLL:
             "lcor_scan_by_key_f64": (i, [i, i, i, vp, vp, vp, vp, u64]),
             "lcor_reduce_by_key": (i, [i, i, i, vp, vp, vp, vp, u64, ctypes.POINTER(u64)]),
             "lcor_reduce_by_key_f64": (i, [i, i, vp, vp, u64, vp, vp, ctypes.POINTER(u64)]),
-            "lcor_segment_reduce": (i, [i, i, vp, vp, u64, vp, vp]),
+            "lcor_segment_reduce": (i, [i, i, vp, vp, u64, vp, vp, vp]),
+            "lcor_segment_reduce_arg": (i, [i, i, vp, vp, vp, u64, vp, vp]),
             "lcor_segment_reduce_f64": (i, [i, vp, u64, vp, vp, vp, vp]),
             "lcor_segment_reduce_mt": (i, [i, vp, vp, u64, vp, vp, i]),
         }
@@ -272,11 +273,34 @@ def reduce_by_key_f64(keys: np.ndarray, values: np.ndarray):
 
 
 # ---------------------------------------------------------------- segment reduce
-def segment_reduce(op: int, a: np.ndarray, begin: np.ndarray, end: np.ndarray) -> np.ndarray:
+def segment_reduce(op: int, a: np.ndarray, begin: np.ndarray, end: np.ndarray, init=None) -> np.ndarray:
+    """out[s] = op(init, fold(a[begin[s]:end[s]])); init None = the op's identity."""
     a = np.ascontiguousarray(a)
+    begin = np.ascontiguousarray(begin, np.uint32)
+    end = np.ascontiguousarray(end, np.uint32)
     out = np.empty(begin.size, a.dtype)
-    _ok(lib().lcor_segment_reduce(op, _code(a), _p(a), _p(out), begin.size, _p(begin), _p(end)), "segment_reduce")
+    iv = np.array([init], dtype=a.dtype) if init is not None else None
+    _ok(lib().lcor_segment_reduce(op, _code(a), _p(a), _p(out), begin.size, _p(begin), _p(end),
+                                  _p(iv) if iv is not None else None), "segment_reduce")
     return out
+
+
+def segment_reduce_arg(is_max: bool, a: np.ndarray, begin: np.ndarray, end: np.ndarray):
+    """(values, relative indices) of ArgMax (is_max) / ArgMin per segment."""
+    a = np.ascontiguousarray(a)
+    begin = np.ascontiguousarray(begin, np.uint32)
+    end = np.ascontiguousarray(end, np.uint32)
+    out = np.empty(begin.size, a.dtype)
+    idx = np.empty(begin.size, np.uint32)
+    _ok(lib().lcor_segment_reduce_arg(int(is_max), _code(a), _p(a), _p(out), _p(idx), begin.size, _p(begin),
+                                      _p(end)), "segment_reduce_arg")
+    return out, idx
+
+
+def fixed_segments(num_segments: int, segment_size: int):
+    """CSR offsets of fixed-size segments: [s * size, (s + 1) * size)."""
+    b = (np.arange(num_segments, dtype=np.uint64) * segment_size).astype(np.uint32)
+    return b, (b.astype(np.uint64) + segment_size).astype(np.uint32)
 
 
 def segment_reduce_f64(a: np.ndarray, begin: np.ndarray, end: np.ndarray):

@@ -117,6 +117,13 @@ def test_unsupported_dtype_and_null_args(L):
     assert L.lcpp_radix_sort_pairs_descending(1, 9, None, 0, None, None, None, None, 10, None) == -3
     assert L.lcpp_radix_sort_pairs_descending(4, 1, None, 0, None, None, None, None, 10, None) == -1
     assert L.lcpp_segment_reduce_sum(2, None, 0, None, None, 10, None, None, None) == -1
+    dummy = ctypes.c_void_p(0x1000)
+    assert L.lcpp_segment_reduce(2, 5, None, 0, dummy, dummy, 10, dummy, dummy, None, None) == -1  # bad op
+    assert L.lcpp_segment_reduce(9, 0, None, 0, dummy, dummy, 10, dummy, dummy, None, None) == -3
+    assert L.lcpp_segment_reduce_fixed(0, 0, None, 0, dummy, dummy, 1 << 20, 1 << 12, None, None) == -1  # >= 2^32
+    assert L.lcpp_segment_reduce_argmin(0, None, 0, dummy, dummy, None, 10, dummy, dummy, None) == -1  # no index_out
+    assert L.lcpp_segment_reduce_argmax_fixed(9, None, 0, dummy, dummy, dummy, 10, 4, None) == -3
+    assert _q(L.lcpp_segment_reduce_arg_temp_bytes, 2, 1 << 27, 1 << 20) == (0, 0)
     assert L.lcpp_scan_exclusive_by_key(0, 0, 0, None, 0, None, None, None, 10, None, None) == -1
     assert L.lcpp_scan_inclusive_by_key(0, 0, 5, None, 0, None, None, None, 10, None, None) == -1  # bad op
     assert L.lcpp_scan_inclusive_sum_by_key(9, 0, None, 0, None, None, None, 10, None) == -3
@@ -179,10 +186,21 @@ int main()
     rs.SortPairsDescending(cl, temp, ki, ko, fi, fo, 10u);
     DeviceSegmentReduce<> sr;
     sr.Sum(cl, temp, fi, fo, 10u, beg, end);
+    sr.Sum(cl, temp, vi, vo, 10u, 32u);
+    sr.Min(cl, temp, fi, fo, 10u, beg, end);
+    sr.Max(cl, temp, vi, vo, 10u, 32u);
+    sr.Reduce(cl, temp, fi, fo, 10u, beg, end, MaxOp{}, 0.f);
+    sr.Reduce(cl, temp, vi, vo, 10u, 7u, SumOp{}, 3);
+    sr.ArgMax(cl, temp, fi, fo, idx, 10u, beg, end);
+    sr.ArgMax(cl, temp, fi, fo, idx, 10u, 32u);
+    sr.ArgMin(cl, temp, vi, vo, idx, 10u, beg, end);
+    sr.Argmin(cl, temp, vi, vo, idx, 10u, beg, end);
+    sr.ArgMin(cl, temp, vi, vo, idx, 10u, 32u);
     return (int)(DeviceReduce<>::GetTempStorageBytes<int>(10) + DeviceScan<>::GetScanByKeyTempStorageBytes<int, float>(10) +
                  DeviceReduce<>::GetReduceByKeyTempStorageBytes<int, float>(10) +
                  DeviceRadixSort<>::GetSortPairsTempStorageBytes<int, float>(10u) +
-                 DeviceSegmentReduce<>::GetTempStorageBytes<float>(10));
+                 DeviceSegmentReduce<>::GetTempStorageBytes<float>(10) +
+                 DeviceSegmentReduce<>::GetArgTempStorageBytes<float>(10, 2));
 }
 """
 

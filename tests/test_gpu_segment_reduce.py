@@ -93,3 +93,135 @@ def test_full_size_c5(gpu):
     empty = b == e
     assert 0.03 < empty.mean() < 0.07
     assert (got[empty].view(np.uint32) == 0).all()  # +0.0 exactly
+
+
+# ------------------------------------------------------------------ Reduce / Min / Max / Arg*, CSR and fixed-size
+ALL_DTYPES = [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64]
+SHUFFLED_1024 = "segment_shuffled_1024_i32.bin"
+
+
+def same(got, ref) -> bool:
+    """Integers bit-exact; floats equal in value (Min/Max of -0.0 and +0.0
+    return either zero depending on the fold order)."""
+    if got.dtype.kind == "f":
+        return bool(np.array_equal(got, ref))
+    return got.tobytes() == ref.tobytes()
+
+
+def seg_call(method, d_in, S, offsets, dtype, *extra, arg=False):
+    """Runs DeviceSegmentReduce.<method>; offsets = (begin, end) host arrays or (segment_size,)."""
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceSegmentReduce
+
+    out = g.empty(S, dtype)
+    idx = g.empty(S, np.uint32) if arg else None
+    off = offsets if isinstance(offsets[0], int) else (g.to_dev(offsets[0]), g.to_dev(offsets[1]))
+    r = DeviceSegmentReduce()
+    if arg:
+        getattr(r, method)(None, d_in, out, idx, S, *off)
+        return g.to_host(out), g.to_host(idx)
+    getattr(r, method)(None, d_in, out, S, *off, *extra)
+    return g.to_host(out)
+
+
+def test_kat_fixed_sum(gpu):
+    # device_segment_reduce.cpp fixed_segment_reduce: 0..1023 in fixed segments of 32
+    import gpu_util as g
+
+    got = seg_call("Sum", g.to_dev(np.arange(1024, dtype=np.int32)), 32, (32,), np.int32)
+    assert (got == np.array([32 * 32 * i + 496 for i in range(32)])).all()
+
+
+def test_kat_argmax_csr_and_fixed_argmin(gpu):
+    # device_segment_reduce.cpp segment_reduce_arg_max (11 segments of <= 100) and
+    # fixed_segment_reduce_arg_min (fixed 32) over the shuffled 0..1023
+    import gpu_util as g
+
+    a = golden(SHUFFLED_1024, np.int32)
+    d = g.to_dev(a)
+    b = np.arange(0, 1024, 100, dtype=np.uint32)
+    e = np.minimum(b + 100, 1024).astype(np.uint32)
+    v, i = seg_call("ArgMax", d, 11, (b, e), np.int32, arg=True)
+    assert (v == np.array([a[x:y].max() for x, y in zip(b, e)])).all()
+    assert (i == np.array([a[x:y].argmax() for x, y in zip(b, e)])).all()
+    v, i = seg_call("ArgMin", d, 32, (32,), np.int32, arg=True)
+    assert (v == a.reshape(32, 32).min(axis=1)).all() and (i == a.reshape(32, 32).argmin(axis=1)).all()
+    v2, i2 = seg_call("Argmin", d, 11, (b, e), np.int32, arg=True)  # the reference's CSR spelling
+    assert (v2 == np.array([a[x:y].min() for x, y in zip(b, e)])).all()
+
+
+@pytest.mark.parametrize("dtype", ALL_DTYPES)
+@pytest.mark.parametrize("op", ["min", "max", "sum"])
+def test_reduce_init_csr_vs_oracle(gpu, dtype, op):
+    import gpu_util as g
+
+    n, S = 400_000, 6000
+    b, e = o.segments(21, 22, n, S)
+    e[::17] = b[::17]  # extra empty segments
+    dt = np.dtype(dtype)
+    a = g.random_array(dtype, n, seed=23)
+    if dt.kind == "f" and op == "sum":
+        a = np.round(a).astype(dt)  # integral values: float sums exact in any order
+    init = dt.type(a[7])
+    log(f"segment Reduce {op} {dt.name}")
+    got = seg_call("Reduce", g.to_dev(a), S, (b, e), dtype, op, init)
+    ref = o.segment_reduce({"sum": o.OP_SUM, "min": o.OP_MIN, "max": o.OP_MAX}[op], a, b, e, init=init)
+    assert same(got, ref)
+    if op != "sum":
+        got = seg_call(op.capitalize(), g.to_dev(a), S, (b, e), dtype)
+        assert same(got, o.segment_reduce({"min": o.OP_MIN, "max": o.OP_MAX}[op], a, b, e))
+
+
+@pytest.mark.parametrize("size", [0, 1, 7, 64, 100, 513, 8192, 8193, 20_000])
+@pytest.mark.parametrize("dtype", [np.int32, np.float64])
+def test_fixed_size_all_ops_vs_oracle(gpu, size, dtype):
+    import gpu_util as g
+
+    S = 600 if size <= 8192 else 150
+    n = max(S * size, 1)
+    dt = np.dtype(dtype)
+    a = g.random_array(dtype, n, seed=size)
+    if dt.kind == "f":
+        a = np.round(a).astype(dt)
+    d = g.to_dev(a)
+    b, e = o.fixed_segments(S, size)
+    log(f"segment fixed size={size} {dt.name}")
+    for method, op in (("Sum", o.OP_SUM), ("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        assert same(seg_call(method, d, S, (size,), dtype), o.segment_reduce(op, a, b, e)), method
+    for method, is_max in (("ArgMin", False), ("ArgMax", True)):
+        v, i = seg_call(method, d, S, (size,), dtype, arg=True)
+        ev, ei = o.segment_reduce_arg(is_max, a, b, e)
+        assert same(v, ev) and (i == ei).all(), method
+
+
+@pytest.mark.parametrize("dtype", ALL_DTYPES)
+def test_arg_csr_ties_empty_long(gpu, dtype):
+    import gpu_util as g
+
+    rng = np.random.default_rng(31)
+    n, S = 1 << 20, 2500
+    b = rng.integers(0, n, S).astype(np.uint32)
+    L = rng.integers(0, 400, S)
+    L[::40] = rng.integers(8193, 60_000, L[::40].size)  # long -> workgroup path
+    L[::9] = 0
+    e = np.minimum(b.astype(np.int64) + L, n).astype(np.uint32)
+    e[::13] = b[::13] // 2  # inverted -> empty
+    a = rng.integers(0, 50, n).astype(dtype)  # many ties
+    d = g.to_dev(a)
+    for method, is_max in (("ArgMin", False), ("ArgMax", True)):
+        log(f"segment {method} {np.dtype(dtype).name}")
+        v, i = seg_call(method, d, S, (b, e), dtype, arg=True)
+        ev, ei = o.segment_reduce_arg(is_max, a, b, e)
+        assert same(v, ev) and (i == ei).all()
+
+
+def test_arg_infinite_and_all_equal(gpu):
+    import gpu_util as g
+
+    a = np.array([-np.inf, -np.inf, np.inf, np.inf, 3, 3, 3], np.float32)
+    b, e = np.array([0, 2, 4, 7], np.uint32), np.array([2, 4, 7, 7], np.uint32)
+    d = g.to_dev(a)
+    v, i = seg_call("ArgMax", d, 4, (b, e), np.float32, arg=True)
+    assert list(i) == [1, 1, 2, 1] and v[0] == -np.inf and v[1] == np.inf and v[3] == np.finfo(np.float32).min
+    v, i = seg_call("ArgMin", d, 4, (b, e), np.float32, arg=True)
+    assert list(i) == [0, 0, 0, 1] and v[3] == np.finfo(np.float32).max

@@ -525,3 +525,87 @@ def test_reduce_by_key_f64_and_edges():
     assert uk.size == 0 and ag.size == 0
     uk, ag = o.reduce_by_key(np.array([5], np.int32), np.array([-7], np.int32))
     assert list(uk) == [5] and list(ag) == [-7]
+
+
+# ------------------------------------------------------------------ segment Min/Max/Arg*, fixed-size
+SHUFFLED_1024 = "segment_shuffled_1024_i32.bin"
+
+
+def test_segment_kat_fixed_sum_closed_form():
+    # device_segment_reduce.cpp fixed_segment_reduce: 0..1023 in segments of 32
+    a = np.arange(1024, dtype=np.int32)
+    b, e = o.fixed_segments(32, 32)
+    assert (o.segment_reduce(o.OP_SUM, a, b, e) == np.array([32 * 32 * i + 496 for i in range(32)])).all()
+
+
+def test_segment_kat_argmax_shuffled():
+    # device_segment_reduce.cpp segment_reduce_arg_max: shuffled 0..1023, 11 segments of <= 100
+    a = golden(SHUFFLED_1024, np.int32)
+    b = np.arange(0, 1024, 100, dtype=np.uint32)
+    e = np.minimum(b + 100, 1024).astype(np.uint32)
+    v, i = o.segment_reduce_arg(True, a, b, e)
+    assert b.size == 11
+    assert (v == np.array([a[x:y].max() for x, y in zip(b, e)])).all()
+    assert (i == np.array([a[x:y].argmax() for x, y in zip(b, e)])).all()
+
+
+def test_segment_kat_fixed_argmin_shuffled():
+    # device_segment_reduce.cpp fixed_segment_reduce_arg_min: shuffled 0..1023, fixed 32
+    a = golden(SHUFFLED_1024, np.int32)
+    b, e = o.fixed_segments(32, 32)
+    v, i = o.segment_reduce_arg(False, a, b, e)
+    assert (v == a.reshape(32, 32).min(axis=1)).all() and (i == a.reshape(32, 32).argmin(axis=1)).all()
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64])
+def test_segment_min_max_init_vs_numpy(dt):
+    b, e = o.segments(11, 12, 50_000, 700)
+    e[::9] = b[::9]  # extra empty segments
+    dt = np.dtype(dt)
+    rng = np.random.default_rng(13)
+    a = (rng.standard_normal(50_000) * 1000).astype(dt) if dt.kind == "f" else \
+        rng.integers(np.iinfo(dt).min, np.iinfo(dt).max, 50_000, dtype=dt, endpoint=True)
+    for op, npop, ident in ((o.OP_MIN, np.min, np.inf), (o.OP_MAX, np.max, -np.inf)):
+        base = dt.type(a[100])
+        got = o.segment_reduce(op, a, b, e, init=base)
+        ref = np.array([npop(np.append(a[x:y], base)) for x, y in zip(b, e)], dt)
+        assert (got == ref).all()
+        got0 = o.segment_reduce(op, a, b, e)
+        lim = (np.finfo(dt) if dt.kind == "f" else np.iinfo(dt))
+        empty_val = lim.max if op == o.OP_MIN else (lim.min if dt.kind != "f" else -lim.max)
+        assert all(g == (npop(a[x:y]) if y > x else empty_val) for g, x, y in zip(got0, b, e))
+
+
+def test_segment_sum_init_wraps():
+    a = np.array([2**31 - 1, 5], np.int32)
+    b, e = np.array([0, 0], np.uint32), np.array([2, 0], np.uint32)
+    assert list(o.segment_reduce(o.OP_SUM, a, b, e, init=np.int32(10))) == [np.int32(-2**31 + 14), 10]
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.float32, np.uint64, np.float64])
+def test_segment_arg_vs_numpy(dt):
+    b, e = o.segments(14, 15, 40_000, 500)
+    e[::13] = b[::13]
+    dt = np.dtype(dt)
+    rng = np.random.default_rng(16)
+    a = rng.integers(0, 40, 40_000).astype(dt)  # many ties
+    vmin, imin = o.segment_reduce_arg(False, a, b, e)
+    vmax, imax = o.segment_reduce_arg(True, a, b, e)
+    lim = np.finfo(dt) if dt.kind == "f" else np.iinfo(dt)
+    for s, (x, y) in enumerate(zip(b, e)):
+        seg = a[x:y]
+        if y <= x:
+            assert imin[s] == 1 and imax[s] == 1 and vmin[s] == lim.max
+            assert vmax[s] == (lim.min if dt.kind != "f" else -lim.max)
+            continue
+        assert imin[s] == seg.argmin() and vmin[s] == seg.min()  # ties: smallest index
+        assert imax[s] == seg.size - 1 - seg[::-1].argmax() and vmax[s] == seg.max()  # ties: largest index
+
+
+def test_segment_arg_infinite_values():
+    a = np.array([-np.inf, -np.inf, np.inf, np.inf], np.float32)
+    b, e = np.array([0, 2], np.uint32), np.array([2, 4], np.uint32)
+    v, i = o.segment_reduce_arg(True, a, b, e)
+    assert list(i) == [1, 1] and v[0] == -np.inf and v[1] == np.inf
+    v, i = o.segment_reduce_arg(False, a, b, e)
+    assert list(i) == [0, 0]
