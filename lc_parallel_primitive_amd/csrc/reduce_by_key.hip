@@ -50,6 +50,10 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
 {
     constexpr int VP = bk_vp<V>();
     constexpr uint32_t TILE = bk_tile<V>();
+    // keys of the tile in LDS when they fit in 32 KiB: the registers that
+    // held them are free for pass 2 (150 -> ~100 VGPRs)
+    constexpr bool kKeysInLds = TILE * sizeof(K) <= 32768;
+    __shared__ K s_keys[kKeysInLds ? TILE : 1];
     __shared__ K s_last[kBkVecs][kBkWaves];
     __shared__ K s_pred;
     __shared__ V s_S[kBkVecs][kBkWaves];
@@ -71,6 +75,12 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
     if (tid < kBkVecs) s_F[tid] = 0;
     K prev0[kBkVecs];
     const uint32_t fl = bk_heads<K, VP>(r.key, prev0, s_last, s_pred, keys, base, tile, tid);
+    if constexpr (kKeysInLds) {
+#pragma unroll
+        for (int k = 0; k < kBkVecs; ++k)
+#pragma unroll
+            for (int j = 0; j < VP; ++j) s_keys[bk_elem<V>(k, tid, j)] = r.key[k][j];
+    }
 
     // pass 1: per vector, (has-head, open fold) pairs and head counts, wave
     // scans of both, wave totals to LDS
@@ -155,7 +165,8 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
                 // from ever writing outside the outputs
                 if (h) {
                     if (gi > 0 && c - 1 < n) {
-                        unique_out[c - 1] = j > 0 ? r.key[k][j - 1] : prev0[k];
+                        if constexpr (kKeysInLds) unique_out[c - 1] = e > 0 ? s_keys[e - 1] : s_pred;
+                        else unique_out[c - 1] = j > 0 ? r.key[k][j - 1] : prev0[k];
                         agg_out[c - 1] = s;
                     }
                     ++c;
@@ -164,7 +175,8 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
                     s = op(s, x);
                 }
                 if (gi == n - 1 && c - 1 < n) {
-                    unique_out[c - 1] = r.key[k][j];
+                    if constexpr (kKeysInLds) unique_out[c - 1] = s_keys[e];
+                    else unique_out[c - 1] = r.key[k][j];
                     agg_out[c - 1] = s;
                     *num_runs = c;
                 }
