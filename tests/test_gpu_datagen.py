@@ -24,3 +24,27 @@ def test_generators_match_host(gpu):
     host = o.gen("normal_f32", n, dg.SEED_SCAN_F32)
     ulps = np.abs(dev.view(np.int32).astype(np.int64) - host.view(np.int32).astype(np.int64))
     assert ulps.max() <= 1 and (ulps == 0).mean() > 0.999
+
+
+@pytest.mark.parametrize("n", [4, 2044, 2048, 2052, 1 << 20, (1 << 20) + 4])
+def test_copy_probe_copies_exactly(gpu, n):
+    """The calibration copy reads and writes exactly n words (guard untouched)."""
+    import torch
+
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen as dg
+
+    src = torch.arange(n + 64, dtype=torch.int32, device="cuda").view(torch.uint32)
+    dst = torch.zeros(n + 64, dtype=torch.int32, device="cuda").view(torch.uint32)
+    dg.copy_probe(src[:n], dst[:n])
+    h = g.to_host(dst.view(torch.int32))
+    assert (h[:n] == np.arange(n)).all() and (h[n:] == 0).all()
+
+
+def test_run_keys_match_host(gpu):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen as dg
+
+    n = 300_007
+    w = o.gen("keys_u32", n, dg.SEED_BY_KEY)
+    assert (g.to_host(dg.run_keys_i32(n, 7)) == np.cumsum((w & 127) == 0, dtype=np.int32)).all()
