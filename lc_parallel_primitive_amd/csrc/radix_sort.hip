@@ -151,6 +151,32 @@ __global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *bins, uint32_t n
     for (uint32_t i = threadIdx.x; i < nbins; i += 256) bins[i] = 0;
 }
 
+// ------------------------------------------------------------------ hot digits
+// hot[p] = the most frequent digit of pass p (the smallest on ties) when it
+// holds at least 1/16 of the keys, else kRadix (none).  One workgroup, one
+// wave per pass at a time.
+__global__ __launch_bounds__(256) void rs_hot_kernel(const uint32_t *__restrict__ bins, uint32_t passes,
+                                                     uint64_t n, uint32_t *__restrict__ hot)
+{
+    const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
+    for (uint32_t p = wave; p < passes; p += 256 / kWave) {
+        // lane l looks at digits l, l + 64, l + 128, l + 192
+        uint64_t best = 0;  // (count << 8) | (255 - digit): max picks the larger count, then the smaller digit
+#pragma unroll
+        for (int q = 0; q < kRadix / kWave; ++q) {
+            const uint32_t d = lane + (uint32_t)q * kWave;
+            const uint64_t c = ((uint64_t)bins[p * kRadix + d] << 8) | (255u - d);
+            best = c > best ? c : best;
+        }
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const uint64_t o = shfl_xor(best, m);
+            best = o > best ? o : best;
+        }
+        if (lane == 0) hot[p] = (best >> 8) * 16 >= n ? 255u - (uint32_t)(best & 255u) : (uint32_t)kRadix;
+    }
+}
+
 // ------------------------------------------------------------------ histogram
 template <class UK>
 constexpr int hist_copies()
@@ -278,7 +304,7 @@ __global__ __launch_bounds__(kOsBlock)
 __attribute__((amdgpu_waves_per_eu(os_waves_per_eu<UK, UV, PAIRS>(), os_waves_per_eu<UK, UV, PAIRS>())))
 void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const UV *__restrict__ vin,
                         UV *__restrict__ vout, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
-                        LbState lb, uint32_t log_run, UK flip)
+                        LbState lb, uint32_t log_run, UK flip, const uint32_t *__restrict__ hot_digits)
 {
     constexpr int TILE = kOsBlock * IPT;
     constexpr int HALF = TILE / 2;
@@ -291,6 +317,7 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
     const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x, log_run);
+    const uint32_t hot_digit = __builtin_amdgcn_readfirstlane(*hot_digits);
     const uint32_t base = tile * (uint32_t)TILE;
     const uint32_t valid = n - base < (uint32_t)TILE ? n - base : (uint32_t)TILE;
 
@@ -321,10 +348,25 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     // 16-bit ranks per register
     uint32_t rank2[IPT / 2];
     uint32_t *cnt = sm.cnt[wave];
+    // Lanes holding the pass's hot digit (skewed inputs: up to a third of the
+    // keys) are represented in the instruction by their lowest lane, which
+    // adds their number; the others rank by position among them.  Every key
+    // still takes one lane of one atomic instruction, in lane order.
+    const uint32_t hot = hot_digit;
+    auto rank_of = [&](uint32_t dd) -> uint32_t {
+        const bool in_hot = dd == hot;
+        const uint64_t m = ballot(in_hot);
+        const uint32_t leader = m ? (uint32_t)__builtin_ctzll(m) : (uint32_t)kWave;
+        uint32_t res = 0;
+        if (!in_hot || lane == leader) res = atomicAdd(&cnt[dd], lane == leader ? (uint32_t)__builtin_popcountll(m) : 1u);
+        if (!m) return res;
+        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)res, (int)leader);
+        return in_hot ? base + mask_rank(m) : res;
+    };
 #pragma unroll
     for (int u = 0; u < IPT; u += 2) {
-        const uint32_t r0 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u], shift, flip)], 1u);
-        const uint32_t r1 = atomicAdd(&cnt[digit_of<UK, KIND>(tk[u + 1], shift, flip)], 1u);
+        const uint32_t r0 = rank_of(digit_of<UK, KIND>(tk[u], shift, flip));
+        const uint32_t r1 = rank_of(digit_of<UK, KIND>(tk[u + 1], shift, flip));
         rank2[u / 2] = r0 | (r1 << 16);
         if ((u & 7) == 6) __builtin_amdgcn_sched_barrier(0);
     }
@@ -473,7 +515,7 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
 constexpr int os_ipt(int key_bytes, int val_bytes) { return key_bytes == 8 || val_bytes == 8 ? 16 : 32; }
 
 struct RsLayout {
-    uint64_t passes, tiles, batches, bins_off, tc_off, tc_words, bw_off, bw_words, ktmp_off, vtmp_off, total;
+    uint64_t passes, tiles, batches, bins_off, hot_off, tc_off, tc_words, bw_off, bw_words, ktmp_off, vtmp_off, total;
 };
 
 RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
@@ -484,7 +526,8 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     L.tiles = n ? ceil_div(n, tile) : 0;
     L.batches = ceil_div(L.tiles, kBatch);
     L.bins_off = 0;
-    L.tc_off = align_up(L.passes * kRadix * 4, 256);
+    L.hot_off = L.passes * kRadix * 4;  // hot digits, one word per pass
+    L.tc_off = align_up(L.hot_off + L.passes * 4, 256);
     L.tc_words = L.tiles * kRadix;
     L.bw_off = L.tc_off + align_up(2 * L.tc_words * 4, 256);
     L.bw_words = L.batches * kRadix;
@@ -526,6 +569,7 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
     char *t = static_cast<char *>(temp);
     uint32_t *bins = reinterpret_cast<uint32_t *>(t + L.bins_off);
+    uint32_t *hot = reinterpret_cast<uint32_t *>(t + L.hot_off);
     uint32_t *tc[2] = {reinterpret_cast<uint32_t *>(t + L.tc_off),
                        reinterpret_cast<uint32_t *>(t + L.tc_off) + L.tc_words};
     uint32_t *bw[2] = {reinterpret_cast<uint32_t *>(t + L.bw_off),
@@ -557,6 +601,8 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
                         kin, n, chunk, bins, tc[0], L.tc_words, bw[0], L.bw_words, flip));
         LCPP_CHECK_LAUNCH();
     }
+    LCPP_LAUNCH("rs_hot", s, rs_hot_kernel<<<1, 256, 0, s>>>(bins, (uint32_t)P, n, hot));
+    LCPP_CHECK_LAUNCH();
     // XCD run length: 8R <= half the onesweep workgroups resident at once
     static uint32_t log_run = 0xFFFFFFFFu;
     if (log_run == 0xFFFFFFFFu) {
@@ -581,7 +627,7 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         LCPP_LAUNCH("rs_onesweep", s,
                     (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
                         src_k, dst_k, src_v, dst_v, (uint32_t)n, (uint32_t)(p * kRadixBits),
-                        bins + p * kRadix, lb, log_run, flip)));
+                        bins + p * kRadix, lb, log_run, flip, hot + p)));
         LCPP_CHECK_LAUNCH();
         src_k = dst_k;
         src_v = dst_v;

@@ -211,3 +211,33 @@ def test_full_size_pairs_u64_descending(gpu):
     ko, vo = sort_pairs(k, v, n, np.uint64, np.uint32, descending=True)
     hk = g.to_host(k)
     assert o.check_stable_pairs_u64_u32(~hk, ~g.to_host(ko), g.to_host(vo))
+
+
+@pytest.mark.parametrize("n", [1, 4097, 100_003, 1 << 20])
+@pytest.mark.parametrize("kdt", [np.uint32, np.int64])
+@pytest.mark.parametrize("descending", [False, True])
+def test_skewed_digits_stable(gpu, n, kdt, descending):
+    """Keys where one digit value dominates every pass (the hot-digit ranking
+    path): 90 % one key, the rest random; values = index check stability."""
+    import gpu_util as g
+
+    rng = np.random.default_rng(n)
+    info = np.iinfo(kdt)
+    k = np.full(n, kdt(0x5A5A5A5A) if info.bits == 32 else kdt(0x1234567890), dtype=kdt)
+    mask = rng.random(n) < 0.1
+    k[mask] = rng.integers(info.min, info.max, mask.sum(), dtype=kdt, endpoint=True)
+    v = np.arange(n, dtype=np.uint32)
+    log(f"skewed pairs n={n} {np.dtype(kdt).name} desc={descending}")
+    ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, kdt, np.uint32, descending=descending)
+    ek, ev = o.radix_sort(k, v, descending=descending)
+    assert same_bits(g.to_host(ko), ek) and same_bits(g.to_host(vo), ev)
+
+
+def test_constant_keys_all_lanes_hot(gpu):
+    import gpu_util as g
+
+    n = (1 << 20) + 77
+    k = np.full(n, 7, np.uint32)
+    v = np.arange(n, dtype=np.uint32)
+    ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, np.uint32, np.uint32)
+    assert (g.to_host(ko) == 7).all() and (g.to_host(vo) == v).all()
