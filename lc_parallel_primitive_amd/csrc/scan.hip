@@ -36,24 +36,36 @@ namespace lcpp {
 namespace {
 
 constexpr int kScanBlock = 256;
-constexpr int kScanVecs = 16;
-template <class T>
+// 16-byte vectors per thread per tile. Measured at 2^28 elements (us per
+// call, 16 / 20 / 24 vectors): exclusive u32 372 / 362 / 368, exclusive i64
+// 744 / 722 / 735; inclusive u32 374 / 377 / 398, inclusive f32 371 / 374 /
+// 364, inclusive i64 741 / 787 / 855. The inclusive integer kernels keep each
+// chunk's wave prefix live until the second pass (integer adds reassociate),
+// so they reach 152 VGPRs (3 workgroups per SIMD) at 20 vectors where the
+// exclusive ones stay at 122 (4 workgroups).
+template <class T, bool INCLUSIVE>
+constexpr int scan_vecs()
+{
+    return !INCLUSIVE ? 20 : (std::is_same<T, float>::value ? 24 : 16);
+}
+template <class T, bool INCLUSIVE>
 constexpr uint32_t scan_tile()
 {
-    return kScanBlock * kScanVecs * (16 / sizeof(T));
+    return kScanBlock * scan_vecs<T, INCLUSIVE>() * (16 / sizeof(T));
 }
 
 // Temp layout: packed look-back words, 8 bytes per tile (32-bit T) or 16
-// bytes per tile (64-bit T).
-template <class T>
+// bytes per tile (64-bit T). The query covers the smaller of the two tiles.
+template <class T, bool INCLUSIVE>
 uint64_t scan_tiles(uint64_t n)
 {
-    return n ? ceil_div(n, scan_tile<T>()) : 0;
+    return n ? ceil_div(n, scan_tile<T, INCLUSIVE>()) : 0;
 }
 template <class T>
 uint64_t scan_temp_bytes(uint64_t n)
 {
-    return align_up(scan_tiles<T>(n) * (sizeof(T) == 4 ? 8 : 16), 256);
+    const uint64_t tiles = std::max(scan_tiles<T, false>(n), scan_tiles<T, true>(n));
+    return align_up(tiles * (sizeof(T) == 4 ? 8 : 16), 256);
 }
 
 template <class T, bool INCLUSIVE>
@@ -62,8 +74,8 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ 
                                                           uint64_t *words, int vec_ok)
 {
     constexpr int V = 16 / sizeof(T);
-    constexpr int K = kScanVecs;
-    constexpr uint32_t TILE = scan_tile<T>();
+    constexpr int K = scan_vecs<T, INCLUSIVE>();
+    constexpr uint32_t TILE = scan_tile<T, INCLUSIVE>();
     constexpr uint32_t CHUNK = kScanBlock * 16;  // bytes per vector instruction
     constexpr int W = kScanBlock / kWave;
     __shared__ T s_wtot[K][W];
@@ -164,7 +176,7 @@ int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, 
     const T *in = static_cast<const T *>(in_);
     T *out = static_cast<T *>(out_);
     if (!in || !out) return LCPP_ERR_INVALID_ARG;
-    const uint64_t tiles = scan_tiles<T>(n);
+    const uint64_t tiles = inclusive ? scan_tiles<T, true>(n) : scan_tiles<T, false>(n);
     if (tiles > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;
     if (temp_bytes < scan_temp_bytes<T>(n)) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;

@@ -70,8 +70,9 @@ def test_temp_bytes_queries(L):
     rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 5, 1 << 28)
     assert rc == 0 and b == 2048 * 16
     assert _q(L.lcpp_reduce_arg_temp_bytes, 0, 100) == (0, 0)
-    # scan: one packed 64-bit word per 16384-element tile (two per 8192-element
-    # tile for 64-bit types)
+    # scan: one packed 64-bit word per tile (two for 64-bit types), counted for
+    # the smaller of the exclusive (20480 / 10240) and inclusive (16384 / 8192;
+    # 24576 for float) integer tiles
     rc, b = _q(L.lcpp_scan_temp_bytes, 1, 1 << 28)
     assert rc == 0 and b == (1 << 14) * 8
     rc, b = _q(L.lcpp_scan_temp_bytes, 4, 1 << 27)

@@ -40,8 +40,11 @@ def test_kat_ones_reused_temp(gpu):
 
 
 @pytest.mark.parametrize("dtype", INT_DTYPES)
-# tiles hold 16384 32-bit / 8192 64-bit elements: cover both boundaries
-@pytest.mark.parametrize("n", [1, 2, 4097, 8191, 8192, 8193, 16383, 16384, 16385, 3 * 16384 + 5, 100_003, 1 << 20])
+# exclusive tiles hold 20480 32-bit / 10240 64-bit elements, inclusive ones 16384 /
+# 8192 (24576 for float): cover every boundary
+@pytest.mark.parametrize("n", [1, 2, 4097, 8191, 8192, 8193, 10239, 10240, 10241, 16383, 16384, 16385,
+                               20479, 20480, 20481, 24575, 24576, 24577, 3 * 16384 + 5,
+                               3 * 20480 + 5, 3 * 24576 + 5, 100_003, 1 << 20])
 @pytest.mark.parametrize("pad", [0, 1])
 def test_integers_vs_oracle(gpu, dtype, n, pad):
     import gpu_util as g
@@ -54,7 +57,7 @@ def test_integers_vs_oracle(gpu, dtype, n, pad):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
-@pytest.mark.parametrize("n", [1, 4097, 1_000_003])
+@pytest.mark.parametrize("n", [1, 4097, 24577, 3 * 24576 + 5, 1_000_003])
 def test_floats_vs_float64(gpu, dtype, n):
     import gpu_util as g
 
@@ -98,7 +101,7 @@ def test_full_size_f32_inclusive(gpu):
 
 
 @pytest.mark.parametrize("dtype", [np.uint32, np.int64])
-@pytest.mark.parametrize("n", [5, 16383, 16385, 3 * 16384 + 7])
+@pytest.mark.parametrize("n", [5, 10241, 16383, 16385, 20479, 24577, 3 * 16384 + 7])
 @pytest.mark.parametrize("pad", [0, 1])
 def test_ragged_tile_writes_nothing_past_the_end(gpu, dtype, n, pad):
     """The last tile's element-wise path stores only [0, n): the output's
