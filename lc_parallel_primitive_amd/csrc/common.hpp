@@ -216,8 +216,10 @@ __device__ __forceinline__ u32x4 pack16(const T (&in)[16 / sizeof(T)])
 // one resource covers < 2 GiB.
 constexpr int kRawBufferWord3 = 0x00020000;
 // Cache-policy operand of the buffer builtins on gfx94x/gfx950: bit 1 = nt
-// (streaming, no reuse expected).
+// (streaming, no reuse expected); bit 4 = sc1 (device scope: the load is
+// served coherently across the XCDs' L2s, as an agent-scope atomic load).
 constexpr int kPolicyNT = 2;
+constexpr int kPolicySc1 = 16;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes)
 {

@@ -43,15 +43,18 @@
 //  * Two-level decoupled look-back.  Tiles form batches of 8.  Each tile
 //    publishes its 256 digit counts once.  A tile's exclusive prefix = the
 //    exclusive prefix of its batch + the counts of the earlier tiles of its
-//    batch (at most 7 parallel reads per digit, by waves 4..7).  The last
-//    tile of a batch publishes the batch aggregate (PARTIAL) as soon as it
-//    has its batch-mates' counts, and the batch's inclusive prefix (GLOBAL)
-//    after a windowed walk over earlier batch words (waves 0..3).  Every
-//    wait is on an earlier tile.  Words are 32-bit {GLOBAL:1 | PARTIAL:1 |
-//    value:30}, accessed with agent-scope atomics (the 8 XCD L2s are not
-//    coherent).  Two look-back regions alternate between passes and each tile
-//    clears its own slots of the other region for the next pass (no per-pass
-//    memset launch).
+//    batch (at most 7 parallel reads per digit, by waves 4..7).  Batch words
+//    carry the batch aggregate and, once its last tile has walked the earlier
+//    batch words (waves 0..3, a window of them per poll), the batch's
+//    inclusive prefix (GLOBAL).  Keys-only passes: 32-bit words {GLOBAL:1 |
+//    PARTIAL:1 | value:30}, the aggregate stored by the batch's last tile as
+//    soon as it has its batch-mates' counts.  Passes that move values: 64-bit
+//    words that every tile adds its counts into atomically.  Every wait is
+//    on an earlier tile, and every re-poll reloads all the words it still
+//    waits on.  Words are accessed with agent-scope atomics (the 8 XCD L2s
+//    are not coherent).  Two look-back regions alternate between passes and
+//    tiles clear their slots of the other region for the next pass (no
+//    per-pass memset launch).
 //  * The sorted tile leaves through LDS in two halves (32 KB of staging
 //    instead of 64 KB), which lets keys-only passes run three workgroups per
 //    CU: consecutive threads write consecutive positions of each digit run.
@@ -70,7 +73,6 @@ constexpr int kRadix = 256;
 constexpr int kOsBlock = 512;  // onesweep workgroup
 constexpr int kOsWaves = kOsBlock / kWave;
 constexpr int kBatch = 8;      // tiles per look-back batch
-constexpr int kBatchWindow = 4;
 constexpr int kHistBlock = 1024;
 constexpr uint32_t kLbGlobal = 0x80000000u;
 constexpr uint32_t kLbPartial = 0x40000000u;
@@ -129,20 +131,63 @@ __device__ __forceinline__ uint32_t digit_excl_scan(uint32_t x, uint32_t *s_wsum
     return pre + inc - x;
 }
 
-// Poll a look-back word until it is published (bounded: a wait that never
-// ends would mean a broken invariant; it then gives up with value 0).
+// Look-back polls are bounded (kSpinLimit re-polls: a wait that never ends
+// would mean a broken invariant; it then gives up with what it has).
 // Agent-scope polls compete with the data stream under full HBM load, so the
 // re-poll interval is long: s_sleep 16 (~1000 cycles) between polls measured
 // 2.17 ms per 2^28 u32 sort against 2.21 ms with s_sleep 1 (s_sleep 64:
 // 2.26 ms); passes that move values prefer s_sleep 4.
-template <int SLEEP>
-__device__ __forceinline__ uint32_t wait_word(const uint32_t *p, uint32_t w)
+//
+// Agent-scope (sc1) loads through a buffer resource: one VGPR offset per
+// load, constant strides folded into the immediate offset (the look-back
+// runs while every key of the tile is held in registers).
+__device__ __forceinline__ uint32_t ld_agent32(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
-    for (uint32_t spins = 0; w == 0 && spins < kSpinLimit; ++spins) {
-        __builtin_amdgcn_s_sleep(SLEEP);
-        w = ld_relaxed(p);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kPolicySc1);
+}
+__device__ __forceinline__ uint64_t ld_agent64(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kPolicySc1);
+    return ((uint64_t)v[1] << 32) | v[0];
+}
+
+// Batch look-back words, two formats.
+//  * Keys-only passes (32-bit): {GLOBAL | PARTIAL | value:30}.  The batch's
+//    last tile stores the batch aggregate (PARTIAL) once it has read its
+//    batch-mates' counts, and later the inclusive prefix (GLOBAL).
+//  * Passes that move values (64-bit): the low half is (tiles arrived << 24)
+//    + their summed digit counts, added atomically by every tile of the batch
+//    as it publishes its own counts, so the aggregate is complete one
+//    publish latency after the batch's last count (no read-and-republish
+//    round trip); the high half is GLOBAL | inclusive prefix, added once by
+//    the batch's last tile.  Measured on SortPairs u64 -> u32 at 2^27: 5.46
+//    -> 5.19 ms.  Keys-only passes keep the 32-bit words: the wider window
+//    registers push the 16384-key tile kernel past its 80-VGPR budget
+//    (2.16 -> 2.21 ms with the resulting spills).
+constexpr uint64_t kBwArrive = 1ull << 24;
+constexpr uint32_t kBwSumMask = (1u << 24) - 1;
+template <bool ATOMIC>
+using batch_word_t = typename std::conditional<ATOMIC, uint64_t, uint32_t>::type;
+template <bool ATOMIC>
+__device__ __forceinline__ batch_word_t<ATOMIC> ld_batch_word(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    if constexpr (ATOMIC) return ld_agent64(r, off);
+    else return ld_agent32(r, off);
+}
+// 0 = not published yet (v = 0; a 64-bit word may already hold the counts of
+// some of its tiles), 1 = batch aggregate in v, 2 = inclusive prefix in v
+template <bool ATOMIC>
+__device__ __forceinline__ int batch_word_state(batch_word_t<ATOMIC> w, uint32_t &v)
+{
+    if constexpr (ATOMIC) {
+        const uint32_t hi = (uint32_t)(w >> 32), lo = (uint32_t)w;
+        const int st = (hi & kLbGlobal) ? 2 : (lo >> 24) == (uint32_t)kBatch ? 1 : 0;
+        v = st == 2 ? hi & kLbMask : st == 1 ? lo & kBwSumMask : 0u;
+        return st;
+    } else {
+        v = w & kLbMask;
+        return (w & kLbGlobal) ? 2 : w ? 1 : 0;
     }
-    return w ? w : kLbGlobal;
 }
 
 // ------------------------------------------------------------------ init
@@ -272,11 +317,13 @@ constexpr int os_waves_per_eu()
 }
 
 // Look-back state of one pass: tcount[tiles][256] (tile digit counts,
-// written once) and bword[batches][256] (batch aggregate, then batch
-// inclusive prefix).
+// written once) and bword[batches][256] (batch aggregate and batch inclusive
+// prefix; 32- or 64-bit words, see batch_word_t).
 struct LbState {
-    uint32_t *tcount, *bword;            // this pass
-    uint32_t *tcount_next, *bword_next;  // the other region, cleared for the next pass
+    uint32_t *tcount;       // this pass
+    void *bword;
+    uint32_t *tcount_next;  // the other region, cleared for the next pass
+    void *bword_next;
 };
 
 // Workgroup -> tile with R = 2^log_run tiles per XCD run: in every full group
@@ -310,6 +357,9 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     constexpr int HALF = TILE / 2;
     constexpr int WAVE_ITEMS = kWave * IPT;
     constexpr int kSleep = PAIRS ? 4 : 16;
+    constexpr bool kAtomicBatch = PAIRS;
+    constexpr int kWindow = PAIRS ? 2 : 4;  // batch words per look-back poll
+    using BW = batch_word_t<kAtomicBatch>;
     static_assert(TILE <= 65536, "tile ranks are packed in 16 bits");
     __shared__ OnesweepSmem<IPT, UK, UV> sm;
 
@@ -394,9 +444,14 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
         }
         if (d == kRadix - 1) total -= (uint32_t)TILE - valid;  // drop the pads
         st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], total | kLbPartial);
+        if constexpr (kAtomicBatch) {
+            if (batch > 0)
+                __hip_atomic_fetch_add(static_cast<BW *>(lb.bword) + (size_t)batch * kRadix + d, kBwArrive + total,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         sm.total[d] = total;
         lb.tcount_next[(size_t)tile * kRadix + d] = 0;
-        if (batch_last) lb.bword_next[(size_t)batch * kRadix + d] = 0;
+        if (bpos == 0) static_cast<BW *>(lb.bword_next)[(size_t)batch * kRadix + d] = 0;
     }
     const uint32_t dexcl = digit_excl_scan(owner ? total : 0u, sm.wsum[0]);
     if (owner) {
@@ -418,49 +473,91 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     }
 
     // ---- two-level look-back.  Waves 4..7 read the counts of the earlier
-    // tiles of the batch (and the batch's last tile publishes the batch
-    // aggregate); waves 0..3 walk the earlier batch words.
+    // tiles of the batch (and, with 32-bit batch words, the batch's last tile
+    // publishes the batch aggregate); waves 0..3 walk the earlier batch words.
+    // Every re-poll (after s_sleep) reloads all the words still unpublished,
+    // so a wait costs one round trip however many words it waits on.
     if (!owner && tid < 2u * kRadix) {
         const uint32_t d2 = tid - kRadix;
-        // branch-free polls: slots k >= bpos re-read this tile's own word
-        const uint32_t *tb = lb.tcount + (size_t)(tile - bpos) * kRadix + d2;
+        const __amdgpu_buffer_rsrc_t rt = make_rsrc(lb.tcount + (size_t)(tile - bpos) * kRadix, kBatch * kRadix * 4);
+        const uint32_t o2 = d2 * 4u;
         uint32_t w7[kBatch - 1];
 #pragma unroll
-        for (int k = 0; k < kBatch - 1; ++k) w7[k] = ld_relaxed(tb + ((uint32_t)k < bpos ? k : bpos) * kRadix);
+        for (int k = 0; k < kBatch - 1; ++k) w7[k] = (uint32_t)k < bpos ? ld_agent32(rt, o2 + k * kRadix * 4) : 1u;
+        for (uint32_t spins = 0; spins < kSpinLimit; ++spins) {
+            bool all = true;
+#pragma unroll
+            for (int k = 0; k < kBatch - 1; ++k) all &= w7[k] != 0;
+            if (all) break;
+            __builtin_amdgcn_s_sleep(kSleep);
+            asm volatile("" ::: "memory");  // the reloads below are new reads
+#pragma unroll
+            for (int k = 0; k < kBatch - 1; ++k)
+                if (w7[k] == 0) w7[k] = ld_agent32(rt, o2 + k * kRadix * 4);
+        }
         uint32_t within = 0;
 #pragma unroll
         for (int k = 0; k < kBatch - 1; ++k)
-            if ((uint32_t)k < bpos) within += wait_word<kSleep>(tb + k * kRadix, w7[k]) & kLbMask;
+            if ((uint32_t)k < bpos) within += w7[k] & kLbMask;
         sm.within[d2] = within;
-        if (batch_last && batch > 0)
-            st_relaxed(&lb.bword[(size_t)batch * kRadix + d2], (within + sm.total[d2]) | kLbPartial);
+        if constexpr (!kAtomicBatch) {
+            if (batch_last && batch > 0)
+                st_relaxed(static_cast<uint32_t *>(lb.bword) + (size_t)batch * kRadix + d2,
+                           (within + sm.total[d2]) | kLbPartial);
+        }
     }
     uint32_t bexcl = gbase;
     if (owner && batch > 0) {
+        // Each poll reads a window of batch words ending at batch j: their
+        // aggregates add up until an inclusive prefix ends the walk; an
+        // unpublished word is where the next poll (after s_sleep) starts.
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(lb.bword, batch * kRadix * (uint32_t)sizeof(BW));
         uint32_t acc = 0;
-        int64_t j = (int64_t)batch - 1;
-        bool done = false;
-        while (!done) {
-            uint32_t w[kBatchWindow];
+        int32_t j = (int32_t)batch - 1;
+        for (uint32_t spins = 0; spins < kSpinLimit; ++spins) {
+            BW w[kWindow];
+            asm volatile("" ::: "memory");  // every poll is a new read
+            if (j >= kWindow - 1) {
+                const uint32_t o = ((uint32_t)(j - (kWindow - 1)) * kRadix + d) * (uint32_t)sizeof(BW);
 #pragma unroll
-            for (int k = 0; k < kBatchWindow; ++k) w[k] = ld_relaxed(&lb.bword[(size_t)(j - k >= 0 ? j - k : 0) * kRadix + d]);
+                for (int k = 0; k < kWindow; ++k)
+                    w[k] = ld_batch_word<kAtomicBatch>(rb, o + (kWindow - 1 - k) * kRadix * (uint32_t)sizeof(BW));
+            } else {
 #pragma unroll
-            for (int k = 0; k < kBatchWindow; ++k) {
-                if (!done) {
-                    const uint32_t wk =
-                        j - k >= 0 ? wait_word<kSleep>(&lb.bword[(size_t)(j - k) * kRadix + d], w[k]) : kLbGlobal;
-                    acc += wk & kLbMask;
-                    done = (wk & kLbGlobal) != 0;
+                for (int k = 0; k < kWindow; ++k)
+                    w[k] = j - k >= 0 ? ld_batch_word<kAtomicBatch>(rb, ((uint32_t)(j - k) * kRadix + d) * (uint32_t)sizeof(BW))
+                                      : BW(0);
+            }
+            bool done = false, stall = false;
+            int adv = 0;
+#pragma unroll
+            for (int k = 0; k < kWindow; ++k) {
+                if (!done && !stall) {
+                    uint32_t v = 0;
+                    const int st = j - k >= 0 ? batch_word_state<kAtomicBatch>(w[k], v) : 2;
+                    stall = st == 0;
+                    done = st == 2;
+                    acc += v;
+                    adv = stall ? adv : k + 1;
                 }
             }
-            j -= kBatchWindow;
+            if (done) break;
+            j -= adv;
+            if (stall) __builtin_amdgcn_s_sleep(kSleep);
         }
         bexcl = acc;
     }
     __syncthreads();
     if (owner) {
         const uint32_t within = sm.within[d];
-        if (batch_last) st_relaxed(&lb.bword[(size_t)batch * kRadix + d], (bexcl + within + total) | kLbGlobal);
+        const uint32_t incl = (bexcl + within + total) | kLbGlobal;
+        if (batch_last) {
+            if constexpr (kAtomicBatch)
+                __hip_atomic_fetch_add(static_cast<BW *>(lb.bword) + (size_t)batch * kRadix + d, (uint64_t)incl << 32,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                st_relaxed(static_cast<uint32_t *>(lb.bword) + (size_t)batch * kRadix + d, incl);
+        }
         sm.goff[d] = bexcl + within - dexcl;
     }
     __syncthreads();
@@ -531,7 +628,7 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     L.tc_words = L.tiles * kRadix;
     L.bw_off = L.tc_off + align_up(2 * L.tc_words * 4, 256);
     L.bw_words = L.batches * kRadix;
-    L.ktmp_off = L.bw_off + align_up(2 * L.bw_words * 4, 256);
+    L.ktmp_off = L.bw_off + align_up(2 * L.bw_words * 8, 256);  // 64-bit words (32-bit ones use half)
     L.vtmp_off = L.ktmp_off + align_up(n * key_bytes, 256);
     L.total = L.vtmp_off + align_up(n * val_bytes, 256);
     return L;
@@ -572,8 +669,8 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     uint32_t *hot = reinterpret_cast<uint32_t *>(t + L.hot_off);
     uint32_t *tc[2] = {reinterpret_cast<uint32_t *>(t + L.tc_off),
                        reinterpret_cast<uint32_t *>(t + L.tc_off) + L.tc_words};
-    uint32_t *bw[2] = {reinterpret_cast<uint32_t *>(t + L.bw_off),
-                       reinterpret_cast<uint32_t *>(t + L.bw_off) + L.bw_words};
+    uint64_t *bw[2] = {reinterpret_cast<uint64_t *>(t + L.bw_off),
+                       reinterpret_cast<uint64_t *>(t + L.bw_off) + L.bw_words};
     UK *ktmp = reinterpret_cast<UK *>(t + L.ktmp_off);
     UV *vtmp = reinterpret_cast<UV *>(t + L.vtmp_off);
     const int P = (int)L.passes;
@@ -598,7 +695,7 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         grid = ceil_div(n, chunk);
         LCPP_LAUNCH("rs_histogram", s,
                     rs_histogram_kernel<UK, KIND><<<(uint32_t)grid, kHistBlock, lds, s>>>(
-                        kin, n, chunk, bins, tc[0], L.tc_words, bw[0], L.bw_words, flip));
+                        kin, n, chunk, bins, tc[0], L.tc_words, reinterpret_cast<uint32_t *>(bw[0]), 2 * L.bw_words, flip));
         LCPP_CHECK_LAUNCH();
     }
     LCPP_LAUNCH("rs_hot", s, rs_hot_kernel<<<1, 256, 0, s>>>(bins, (uint32_t)P, n, hot));

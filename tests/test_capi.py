@@ -77,12 +77,13 @@ def test_temp_bytes_queries(L):
     assert rc == 0 and b == (1 << 14) * 8
     rc, b = _q(L.lcpp_scan_temp_bytes, 4, 1 << 27)
     assert rc == 0 and b == (1 << 14) * 16
-    # sort: bins + hot digits + 2 regions of tile counts + 2 regions of batch words + key
-    # scratch (no value scratch for keys-only); 16384-key tiles, batches of 8
+    # sort: bins + hot digits + 2 regions of tile counts + 2 regions of batch words (8 bytes
+    # each; keys-only passes use 4) + key scratch (no value scratch for keys-only);
+    # 16384-key tiles, batches of 8
     rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, 1 << 28)
     tiles = (1 << 28) // 16384
     bins_and_hot = (4 * 256 * 4 + 4 * 4 + 255) // 256 * 256  # digit bins + one hot digit per pass
-    assert rc == 0 and b == bins_and_hot + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 4 + (1 << 28) * 4
+    assert rc == 0 and b == bins_and_hot + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 8 + (1 << 28) * 4
     rc, bp = _q(L.lcpp_radix_sort_pairs_temp_bytes, 4, 1, 1 << 27)
     assert rc == 0 and bp > (1 << 27) * 12
     # scan by key: one packed word per 8192-value tile (two for 8-byte values)
