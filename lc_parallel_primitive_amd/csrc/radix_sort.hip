@@ -43,18 +43,16 @@
 //  * Two-level decoupled look-back.  Tiles form batches of 8.  Each tile
 //    publishes its 256 digit counts once.  A tile's exclusive prefix = the
 //    exclusive prefix of its batch + the counts of the earlier tiles of its
-//    batch (at most 7 parallel reads per digit, by waves 4..7).  Batch words
-//    carry the batch aggregate and, once its last tile has walked the earlier
-//    batch words (waves 0..3, a window of them per poll), the batch's
-//    inclusive prefix (GLOBAL).  Keys-only passes: 32-bit words {GLOBAL:1 |
-//    PARTIAL:1 | value:30}, the aggregate stored by the batch's last tile as
-//    soon as it has its batch-mates' counts.  Passes that move values: 64-bit
-//    words that every tile adds its counts into atomically.  Every wait is
-//    on an earlier tile, and every re-poll reloads all the words it still
-//    waits on.  Words are accessed with agent-scope atomics (the 8 XCD L2s
-//    are not coherent).  Two look-back regions alternate between passes and
-//    tiles clear their slots of the other region for the next pass (no
-//    per-pass memset launch).
+//    batch (at most 7 parallel reads per digit, by waves 4..7).  Tile counts
+//    are 32-bit words {PARTIAL:1 | value}.  Batch words are 64-bit: every tile
+//    of the batch adds its counts into the low half atomically, and the
+//    batch's last tile, once it has walked the earlier batch words (waves
+//    0..3, two of them per poll), adds GLOBAL | the batch's inclusive prefix
+//    into the high half.  Every wait is on an earlier tile, and every re-poll
+//    reloads all the words it still waits on.  Words are accessed with
+//    agent-scope atomics (the 8 XCD L2s are not coherent).  Two look-back
+//    regions alternate between passes and tiles clear their slots of the
+//    other region for the next pass (no per-pass memset launch).
 //  * The sorted tile leaves through LDS in two halves (32 KB of staging
 //    instead of 64 KB), which lets keys-only passes run three workgroups per
 //    CU: consecutive threads write consecutive positions of each digit run.
@@ -151,43 +149,25 @@ __device__ __forceinline__ uint64_t ld_agent64(__amdgpu_buffer_rsrc_t r, uint32_
     return ((uint64_t)v[1] << 32) | v[0];
 }
 
-// Batch look-back words, two formats.
-//  * Keys-only passes (32-bit): {GLOBAL | PARTIAL | value:30}.  The batch's
-//    last tile stores the batch aggregate (PARTIAL) once it has read its
-//    batch-mates' counts, and later the inclusive prefix (GLOBAL).
-//  * Passes that move values (64-bit): the low half is (tiles arrived << 24)
-//    + their summed digit counts, added atomically by every tile of the batch
-//    as it publishes its own counts, so the aggregate is complete one
-//    publish latency after the batch's last count (no read-and-republish
-//    round trip); the high half is GLOBAL | inclusive prefix, added once by
-//    the batch's last tile.  Measured on SortPairs u64 -> u32 at 2^27: 5.46
-//    -> 5.19 ms.  Keys-only passes keep the 32-bit words: the wider window
-//    registers push the 16384-key tile kernel past its 80-VGPR budget
-//    (2.16 -> 2.21 ms with the resulting spills).
+// Batch look-back words, 64-bit.  The low half is (tiles arrived << 24) +
+// their summed digit counts: every tile of the batch adds its counts with a
+// relaxed agent-scope atomic as it publishes them, so the batch aggregate is
+// complete one publish latency after the batch's last count, with no
+// read-and-republish round trip by one of its tiles.  The high half is
+// GLOBAL | inclusive prefix through the batch, added once by the batch's last
+// tile.  Measured at 2^28 u32 keys against 32-bit {GLOBAL | PARTIAL | value}
+// words stored by the batch's last tile: 2.13 -> 2.05 ms per sort (AND-of-3
+// keys 2.15 -> 2.03 ms); SortPairs u64 -> u32 at 2^27: 5.42 -> 5.19 ms.
 constexpr uint64_t kBwArrive = 1ull << 24;
 constexpr uint32_t kBwSumMask = (1u << 24) - 1;
-template <bool ATOMIC>
-using batch_word_t = typename std::conditional<ATOMIC, uint64_t, uint32_t>::type;
-template <bool ATOMIC>
-__device__ __forceinline__ batch_word_t<ATOMIC> ld_batch_word(__amdgpu_buffer_rsrc_t r, uint32_t off)
+// 0 = not complete yet (v = 0: the word may hold the counts of some of its
+// tiles), 1 = batch aggregate in v, 2 = inclusive prefix in v
+__device__ __forceinline__ int batch_word_state(uint64_t w, uint32_t &v)
 {
-    if constexpr (ATOMIC) return ld_agent64(r, off);
-    else return ld_agent32(r, off);
-}
-// 0 = not published yet (v = 0; a 64-bit word may already hold the counts of
-// some of its tiles), 1 = batch aggregate in v, 2 = inclusive prefix in v
-template <bool ATOMIC>
-__device__ __forceinline__ int batch_word_state(batch_word_t<ATOMIC> w, uint32_t &v)
-{
-    if constexpr (ATOMIC) {
-        const uint32_t hi = (uint32_t)(w >> 32), lo = (uint32_t)w;
-        const int st = (hi & kLbGlobal) ? 2 : (lo >> 24) == (uint32_t)kBatch ? 1 : 0;
-        v = st == 2 ? hi & kLbMask : st == 1 ? lo & kBwSumMask : 0u;
-        return st;
-    } else {
-        v = w & kLbMask;
-        return (w & kLbGlobal) ? 2 : w ? 1 : 0;
-    }
+    const uint32_t hi = (uint32_t)(w >> 32), lo = (uint32_t)w;
+    const int st = (hi & kLbGlobal) ? 2 : (lo >> 24) == (uint32_t)kBatch ? 1 : 0;
+    v = st == 2 ? hi & kLbMask : st == 1 ? lo & kBwSumMask : 0u;
+    return st;
 }
 
 // ------------------------------------------------------------------ init
@@ -318,12 +298,12 @@ constexpr int os_waves_per_eu()
 
 // Look-back state of one pass: tcount[tiles][256] (tile digit counts,
 // written once) and bword[batches][256] (batch aggregate and batch inclusive
-// prefix; 32- or 64-bit words, see batch_word_t).
+// prefix, see batch_word_state).
 struct LbState {
     uint32_t *tcount;       // this pass
-    void *bword;
+    uint64_t *bword;
     uint32_t *tcount_next;  // the other region, cleared for the next pass
-    void *bword_next;
+    uint64_t *bword_next;
 };
 
 // Workgroup -> tile with R = 2^log_run tiles per XCD run: in every full group
@@ -357,9 +337,9 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     constexpr int HALF = TILE / 2;
     constexpr int WAVE_ITEMS = kWave * IPT;
     constexpr int kSleep = PAIRS ? 4 : 16;
-    constexpr bool kAtomicBatch = PAIRS;
-    constexpr int kWindow = PAIRS ? 2 : 4;  // batch words per look-back poll
-    using BW = batch_word_t<kAtomicBatch>;
+    // batch words per look-back poll: 2 keeps the 16384-key kernel within
+    // 80 VGPRs (a window of 4 spills 20 VGPRs: 2.59 ms per sort; 3: same as 2)
+    constexpr int kWindow = 2;
     static_assert(TILE <= 65536, "tile ranks are packed in 16 bits");
     __shared__ OnesweepSmem<IPT, UK, UV> sm;
 
@@ -444,14 +424,13 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
         }
         if (d == kRadix - 1) total -= (uint32_t)TILE - valid;  // drop the pads
         st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], total | kLbPartial);
-        if constexpr (kAtomicBatch) {
-            if (batch > 0)
-                __hip_atomic_fetch_add(static_cast<BW *>(lb.bword) + (size_t)batch * kRadix + d, kBwArrive + total,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        // batch 0's word only ever carries its inclusive prefix
+        if (batch > 0)
+            __hip_atomic_fetch_add(&lb.bword[(size_t)batch * kRadix + d], kBwArrive + total, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         sm.total[d] = total;
         lb.tcount_next[(size_t)tile * kRadix + d] = 0;
-        if (bpos == 0) static_cast<BW *>(lb.bword_next)[(size_t)batch * kRadix + d] = 0;
+        if (bpos == 0) lb.bword_next[(size_t)batch * kRadix + d] = 0;
     }
     const uint32_t dexcl = digit_excl_scan(owner ? total : 0u, sm.wsum[0]);
     if (owner) {
@@ -473,8 +452,7 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     }
 
     // ---- two-level look-back.  Waves 4..7 read the counts of the earlier
-    // tiles of the batch (and, with 32-bit batch words, the batch's last tile
-    // publishes the batch aggregate); waves 0..3 walk the earlier batch words.
+    // tiles of the batch; waves 0..3 walk the earlier batch words.
     // Every re-poll (after s_sleep) reloads all the words still unpublished,
     // so a wait costs one round trip however many words it waits on.
     if (!owner && tid < 2u * kRadix) {
@@ -500,33 +478,26 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
         for (int k = 0; k < kBatch - 1; ++k)
             if ((uint32_t)k < bpos) within += w7[k] & kLbMask;
         sm.within[d2] = within;
-        if constexpr (!kAtomicBatch) {
-            if (batch_last && batch > 0)
-                st_relaxed(static_cast<uint32_t *>(lb.bword) + (size_t)batch * kRadix + d2,
-                           (within + sm.total[d2]) | kLbPartial);
-        }
     }
     uint32_t bexcl = gbase;
     if (owner && batch > 0) {
         // Each poll reads a window of batch words ending at batch j: their
         // aggregates add up until an inclusive prefix ends the walk; an
         // unpublished word is where the next poll (after s_sleep) starts.
-        const __amdgpu_buffer_rsrc_t rb = make_rsrc(lb.bword, batch * kRadix * (uint32_t)sizeof(BW));
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(lb.bword, batch * kRadix * 8u);
         uint32_t acc = 0;
         int32_t j = (int32_t)batch - 1;
         for (uint32_t spins = 0; spins < kSpinLimit; ++spins) {
-            BW w[kWindow];
+            uint64_t w[kWindow];
             asm volatile("" ::: "memory");  // every poll is a new read
             if (j >= kWindow - 1) {
-                const uint32_t o = ((uint32_t)(j - (kWindow - 1)) * kRadix + d) * (uint32_t)sizeof(BW);
+                const uint32_t o = ((uint32_t)(j - (kWindow - 1)) * kRadix + d) * 8u;
 #pragma unroll
-                for (int k = 0; k < kWindow; ++k)
-                    w[k] = ld_batch_word<kAtomicBatch>(rb, o + (kWindow - 1 - k) * kRadix * (uint32_t)sizeof(BW));
+                for (int k = 0; k < kWindow; ++k) w[k] = ld_agent64(rb, o + (kWindow - 1 - k) * kRadix * 8u);
             } else {
 #pragma unroll
                 for (int k = 0; k < kWindow; ++k)
-                    w[k] = j - k >= 0 ? ld_batch_word<kAtomicBatch>(rb, ((uint32_t)(j - k) * kRadix + d) * (uint32_t)sizeof(BW))
-                                      : BW(0);
+                    w[k] = j - k >= 0 ? ld_agent64(rb, ((uint32_t)(j - k) * kRadix + d) * 8u) : 0ull;
             }
             bool done = false, stall = false;
             int adv = 0;
@@ -534,7 +505,7 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
             for (int k = 0; k < kWindow; ++k) {
                 if (!done && !stall) {
                     uint32_t v = 0;
-                    const int st = j - k >= 0 ? batch_word_state<kAtomicBatch>(w[k], v) : 2;
+                    const int st = j - k >= 0 ? batch_word_state(w[k], v) : 2;
                     stall = st == 0;
                     done = st == 2;
                     acc += v;
@@ -551,13 +522,9 @@ void rs_onesweep_kernel(const UK *__restrict__ kin, UK *__restrict__ kout, const
     if (owner) {
         const uint32_t within = sm.within[d];
         const uint32_t incl = (bexcl + within + total) | kLbGlobal;
-        if (batch_last) {
-            if constexpr (kAtomicBatch)
-                __hip_atomic_fetch_add(static_cast<BW *>(lb.bword) + (size_t)batch * kRadix + d, (uint64_t)incl << 32,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else
-                st_relaxed(static_cast<uint32_t *>(lb.bword) + (size_t)batch * kRadix + d, incl);
-        }
+        if (batch_last)
+            __hip_atomic_fetch_add(&lb.bword[(size_t)batch * kRadix + d], (uint64_t)incl << 32, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         sm.goff[d] = bexcl + within - dexcl;
     }
     __syncthreads();
@@ -628,7 +595,7 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     L.tc_words = L.tiles * kRadix;
     L.bw_off = L.tc_off + align_up(2 * L.tc_words * 4, 256);
     L.bw_words = L.batches * kRadix;
-    L.ktmp_off = L.bw_off + align_up(2 * L.bw_words * 8, 256);  // 64-bit words (32-bit ones use half)
+    L.ktmp_off = L.bw_off + align_up(2 * L.bw_words * 8, 256);  // 64-bit words
     L.vtmp_off = L.ktmp_off + align_up(n * key_bytes, 256);
     L.total = L.vtmp_off + align_up(n * val_bytes, 256);
     return L;
