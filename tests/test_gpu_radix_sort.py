@@ -117,6 +117,30 @@ def test_pairs_stable_vs_oracle(gpu, kdt, vdt, n):
     assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
 
 
+# Tiles hold 16384 keys (8192 when keys or values are 8 bytes) and the look-back
+# groups them in batches of 8: sizes around 1, 2, 3 and 5 batches, ragged and exact.
+@pytest.mark.parametrize("kdt,vdt", [(np.uint32, None), (np.uint64, None), (np.uint32, np.uint32),
+                                     (np.uint64, np.uint32)])
+@pytest.mark.parametrize("tiles,delta", [(7, 0), (8, -1), (8, 0), (8, 1), (9, 0), (16, 0), (17, 5),
+                                         (24, -3), (40, 7)])
+def test_lookback_batch_boundaries(gpu, kdt, vdt, tiles, delta):
+    import gpu_util as g
+
+    tile = 8192 if np.dtype(kdt).itemsize == 8 or (vdt is not None and np.dtype(vdt).itemsize == 8) else 16384
+    n = tiles * tile + delta
+    k = g.random_array(kdt, n, seed=tiles * 7 + delta)
+    log(f"sort batch boundaries {np.dtype(kdt).name}/{vdt and np.dtype(vdt).name} n={n}")
+    if vdt is None:
+        got = g.to_host(sort_keys(g.to_dev(k), n, kdt))
+        assert same_bits(got, o.radix_sort(k))
+    else:
+        k = k & np.array(0xFFF, dtype=kdt)  # duplicates: stability across tiles and batches
+        v = np.arange(n, dtype=vdt)
+        ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, kdt, vdt)
+        rk, rv = o.radix_sort(k, v)
+        assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
+
+
 @pytest.mark.parametrize("dtype", KEY_DTYPES)
 @pytest.mark.parametrize("n", [1, 65, 4097, 16385, 100_003])
 def test_keys_descending_vs_oracle(gpu, dtype, n):
