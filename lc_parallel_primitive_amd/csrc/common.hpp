@@ -101,6 +101,42 @@ __device__ __forceinline__ T read_lane(T x, int lane)
     }
 }
 
+// DPP permutation of a 4- or 8-byte value inside each row of 16 lanes
+// (a VALU operand modifier: no LDS round trip, unlike __shfl_xor, which
+// lowers to ds_bpermute_b32).
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppRowHalfMirror = 0x141; // lane i <-> 7 - i within each 8
+constexpr int kDppRowMirror = 0x140;     // lane i <-> 15 - i within each 16
+template <int CTRL, class T>
+__device__ __forceinline__ T dpp_perm(T x)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+    } else {
+        static_assert(sizeof(T) == 8, "4- or 8-byte types only");
+        int2 v = __builtin_bit_cast(int2, x);
+        v.x = __builtin_amdgcn_update_dpp(0, v.x, CTRL, 0xF, 0xF, false);
+        v.y = __builtin_amdgcn_update_dpp(0, v.y, CTRL, 0xF, 0xF, false);
+        return __builtin_bit_cast(T, v);
+    }
+}
+
+// Reduction over the 64 lanes whose result is wave-uniform: DPP steps make
+// every lane of a row of 16 hold the row's fold (pairs: lane ^ 1, lane ^ 2,
+// then the two quads of each 8, then the two 8s of each 16), and the four row
+// folds are read out of lanes 0, 16, 32, 48.  `op` must be commutative and
+// associative (the pairing differs from a butterfly).
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce_dpp(T x, Op op)
+{
+    x = op(x, dpp_perm<kDppQuadXor1>(x));
+    x = op(x, dpp_perm<kDppQuadXor2>(x));
+    x = op(x, dpp_perm<kDppRowHalfMirror>(x));
+    x = op(x, dpp_perm<kDppRowMirror>(x));
+    return op(op(read_lane(x, 0), read_lane(x, 16)), op(read_lane(x, 32), read_lane(x, 48)));
+}
+
 // Butterfly all-reduce over the 64 lanes; every lane gets the result.
 template <class T, class Op>
 __device__ __forceinline__ T wave_allreduce(T x, Op op)
