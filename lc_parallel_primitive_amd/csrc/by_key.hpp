@@ -63,16 +63,19 @@ __device__ __forceinline__ void seg_fold(bool &fa, T &a, bool fb, T b, Op op)
 template <class T, class Op>
 __device__ __forceinline__ void wave_seg_scan(bool &f, T &s, Op op)
 {
-    const uint32_t lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int fu = __shfl_up((int)f, d);
-        const T su = shfl_up(s, d);
-        if (lane >= (uint32_t)d) {
-            s = f ? s : op(su, s);
-            f = f || fu;
-        }
-    }
+    // the DPP steps of wave_inclusive_scan over (flag, value) pairs; lanes
+    // with no source take (false, identity)
+    const T id = op_identity<Op, T>();
+    auto step = [&](int fu, T su) {
+        s = f ? s : op(su, s);
+        f = f || fu != 0;
+    };
+    step(dpp_move<kDppRowShr + 1>((int)f, 0), dpp_move<kDppRowShr + 1>(s, id));
+    step(dpp_move<kDppRowShr + 2>((int)f, 0), dpp_move<kDppRowShr + 2>(s, id));
+    step(dpp_move<kDppRowShr + 4>((int)f, 0), dpp_move<kDppRowShr + 4>(s, id));
+    step(dpp_move<kDppRowShr + 8>((int)f, 0), dpp_move<kDppRowShr + 8>(s, id));
+    step(dpp_move<kDppRowBcast15, 0xA>((int)f, 0), dpp_move<kDppRowBcast15, 0xA>(s, id));
+    step(dpp_move<kDppRowBcast31, 0xC>((int)f, 0), dpp_move<kDppRowBcast31, 0xC>(s, id));
 }
 
 // Keys and values of one thread.

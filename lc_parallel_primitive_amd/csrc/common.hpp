@@ -106,20 +106,32 @@ __device__ __forceinline__ T read_lane(T x, int lane)
 // lowers to ds_bpermute_b32).
 constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]: lane ^ 1
 constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]: lane ^ 2
-constexpr int kDppRowHalfMirror = 0x141; // lane i <-> 7 - i within each 8
+constexpr int kDppRowShr = 0x110;        // + n: lane i <- lane i - n inside its row of 16
+constexpr int kDppWaveShr1 = 0x138;      // lane i <- lane i - 1 across the wave
 constexpr int kDppRowMirror = 0x140;     // lane i <-> 15 - i within each 16
+constexpr int kDppRowHalfMirror = 0x141; // lane i <-> 7 - i within each 8
+constexpr int kDppRowBcast15 = 0x142;    // row r + 1 <- lane 15 of row r
+constexpr int kDppRowBcast31 = 0x143;    // rows 2 and 3 <- lane 31
+// Lanes whose source is outside the pattern, or whose row is not in
+// ROW_MASK, get `old`.
+template <int CTRL, int ROW_MASK = 0xF, class T>
+__device__ __forceinline__ T dpp_move(T x, T old)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, x),
+                                                                 CTRL, ROW_MASK, 0xF, false));
+    } else {
+        static_assert(sizeof(T) == 8, "4- or 8-byte types only");
+        int2 v = __builtin_bit_cast(int2, x), o = __builtin_bit_cast(int2, old);
+        v.x = __builtin_amdgcn_update_dpp(o.x, v.x, CTRL, ROW_MASK, 0xF, false);
+        v.y = __builtin_amdgcn_update_dpp(o.y, v.y, CTRL, ROW_MASK, 0xF, false);
+        return __builtin_bit_cast(T, v);
+    }
+}
 template <int CTRL, class T>
 __device__ __forceinline__ T dpp_perm(T x)
 {
-    if constexpr (sizeof(T) == 4) {
-        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
-    } else {
-        static_assert(sizeof(T) == 8, "4- or 8-byte types only");
-        int2 v = __builtin_bit_cast(int2, x);
-        v.x = __builtin_amdgcn_update_dpp(0, v.x, CTRL, 0xF, 0xF, false);
-        v.y = __builtin_amdgcn_update_dpp(0, v.y, CTRL, 0xF, 0xF, false);
-        return __builtin_bit_cast(T, v);
-    }
+    return dpp_move<CTRL>(x, T(0));
 }
 
 // Reduction over the 64 lanes whose result is wave-uniform: DPP steps make
@@ -137,26 +149,40 @@ __device__ __forceinline__ T wave_reduce_dpp(T x, Op op)
     return op(op(read_lane(x, 0), read_lane(x, 16)), op(read_lane(x, 32), read_lane(x, 48)));
 }
 
-// Butterfly all-reduce over the 64 lanes; every lane gets the result.
+// All-reduce over the 64 lanes; every lane gets the result (wave_reduce_dpp:
+// the same pairing as a lane ^ 1, ^ 2, ... butterfly, so float sums are
+// bit-identical to one).  `op` must be commutative and associative.
 template <class T, class Op>
 __device__ __forceinline__ T wave_allreduce(T x, Op op)
 {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) x = op(x, shfl_xor(x, m));
-    return x;
+    return wave_reduce_dpp(x, op);
 }
 
-// Kogge-Stone inclusive scan over the 64 lanes (lane order).
+// Inclusive scan over the 64 lanes (lane order) with DPP: Kogge-Stone
+// inside each row of 16 (row_shr 1, 2, 4, 8), then row 0's total into row 1
+// and row 2's into row 3 (row_bcast15), then the first half's total into
+// rows 2 and 3 (row_bcast31).  Lanes with no source take Op's identity.
+// 6 VALU steps (the DPP folds into the op's instruction for 4-byte types);
+// the __shfl_up form took 6 ds_bpermute round trips (64-bit scans: 757 us
+// with it against 744 us, both at 2^27).
 template <class T, class Op>
 __device__ __forceinline__ T wave_inclusive_scan(T x, Op op)
 {
-    const uint32_t lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        T y = shfl_up(x, d);
-        if (lane >= (uint32_t)d) x = op(y, x);
-    }
+    const T id = Op::template identity<T>();
+    x = op(dpp_move<kDppRowShr + 1>(x, id), x);
+    x = op(dpp_move<kDppRowShr + 2>(x, id), x);
+    x = op(dpp_move<kDppRowShr + 4>(x, id), x);
+    x = op(dpp_move<kDppRowShr + 8>(x, id), x);
+    x = op(dpp_move<kDppRowBcast15, 0xA>(x, id), x);
+    x = op(dpp_move<kDppRowBcast31, 0xC>(x, id), x);
     return x;
+}
+
+// x of lane - 1 (lane 0: `fill`), a DPP wave shift.
+template <class T>
+__device__ __forceinline__ T wave_shr1(T x, T fill)
+{
+    return dpp_move<kDppWaveShr1>(x, fill);
 }
 
 // ---------------------------------------------------------------- atomics

@@ -68,8 +68,19 @@ uint64_t scan_temp_bytes(uint64_t n)
     return align_up(tiles * (sizeof(T) == 4 ? 8 : 16), 256);
 }
 
+// 4-byte integer kernels are held to 128 VGPRs (4 workgroups per SIMD):
+// with the DPP wave scan the compiler otherwise takes 132 (exclusive u32, 20
+// vectors; the scan slows from 357 to 367 us) or 134 (inclusive).  The
+// inclusive float kernel (24 vectors) would spill, and the 64-bit kernels
+// stay under 128 anyway but measured 3 % slower with the limit.
 template <class T, bool INCLUSIVE>
-__global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ in,
+constexpr int scan_min_waves()
+{
+    return sizeof(T) == 4 && !(INCLUSIVE && std::is_same<T, float>::value) ? 4 : 1;
+}
+template <class T, bool INCLUSIVE>
+__global__ __launch_bounds__(kScanBlock) __attribute__((amdgpu_waves_per_eu(scan_min_waves<T, INCLUSIVE>())))
+void scan_kernel(const T *__restrict__ in,
                                                           T *__restrict__ out, uint64_t n,
                                                           uint64_t *words, int vec_ok)
 {
@@ -123,8 +134,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_kernel(const T *__restrict__ 
             }
         }
         const T inc = wave_inclusive_scan(r, op);
-        const T up = shfl_up(inc, 1);
-        const T wex = lane == 0 ? T(0) : up;
+        const T wex = wave_shr1(inc, T(0));
         if (lane == kWave - 1) s_wtot[k][wave] = inc;
 #pragma unroll
         for (int j = 0; j < V; ++j) x[k][j] = op(wex, x[k][j]);
