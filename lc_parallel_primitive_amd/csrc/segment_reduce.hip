@@ -22,6 +22,12 @@
 //    LDS and the whole workgroup streams each one (4 loads in flight per
 //    thread) after its waves are done.  Fixed-size segments longer than
 //    kSegLong take a workgroup-per-segment launch directly.
+//  * Flat path: a wave whose 64 segments tile one contiguous range (CSR
+//    offsets with end[s] == begin[s + 1], or fixed-size segments), none of
+//    them long, streams that range in 4 KiB chunks of coalesced 16-byte
+//    loads, transposes each chunk through LDS so that every lane holds
+//    consecutive elements, folds them in order and joins the lanes with a
+//    segmented scan (flat_segments below).
 //  * Sum/Min/Max write op(init, fold) (init defaults to the operator's
 //    identity; Min starts from max(), Max from lowest()); an empty segment
 //    (end <= begin, or segment_size 0) writes init.  Arg* keep
@@ -47,7 +53,9 @@ constexpr int kSegWaves = kSegBlock / kWave;
 // grid of waves striding over groups of 8 measured 141-190 us, and 16-byte
 // vector loads with index masking 127 us (fewer waves fit).  The per-segment
 // wave reductions use DPP and readlane instead of __shfl_xor (ds_bpermute
-// through LDS): 119-122 -> 113 us.
+// through LDS): 119-122 -> 113 us.  The flat path takes C5 to 104-105 us (a
+// copy of it that only sums each wave's range, with no segment logic, runs
+// in 87.5 us).
 constexpr int kSegGroup = 8;
 constexpr int kSegPerWave = 64;
 constexpr uint32_t kSegLong = 8192;
@@ -110,6 +118,13 @@ struct SegAcc {
     {
         if constexpr (kArg) return A{dpp_perm<CTRL>(a.value), dpp_perm<CTRL>(a.index)};
         else return dpp_perm<CTRL>(a);
+    }
+    template <int CTRL, int ROW_MASK>
+    static __device__ __forceinline__ A dpp_mv(A a, A old)
+    {
+        if constexpr (kArg)
+            return A{dpp_move<CTRL, ROW_MASK>(a.value, old.value), dpp_move<CTRL, ROW_MASK>(a.index, old.index)};
+        else return dpp_move<CTRL, ROW_MASK>(a, old);
     }
     static __device__ __forceinline__ A readlane_acc(A a, int l)
     {
@@ -202,10 +217,160 @@ __device__ __forceinline__ void wg_reduce_segment(const T *__restrict__ in, T *_
     __syncthreads();
 }
 
+// ---- flat path: a wave whose 64 segments tile one contiguous range
+// [B, E) streams that range in chunks with coalesced 16-byte loads instead
+// of walking its segments 8 at a time (24 dependent load round trips per
+// wave for mean length 128).  Each chunk goes through LDS so that lane l
+// then holds kFlatEpl consecutive elements; the lane folds them in order,
+// writing every segment that starts and ends inside it.  The open segment
+// at each lane's start comes from a segmented scan across the lanes (plus
+// the open segment carried from the previous chunk): with it a lane writes
+// the first segment that ends inside it.  The last segment of the range is
+// written after the last chunk, empty segments at the start.  Per segment the
+// fold order is the element order: first the lanes before, then the lane's
+// own elements.
+template <class T>
+constexpr int flat_epl()
+{
+    return 64 / (int)sizeof(T);  // 4 KiB of elements per wave per chunk
+}
+template <class T>
+struct FlatSmem {
+    uint32_t bnd[kSegWaves][kSegPerWave + 1];
+    T stage[kSegWaves][kWave * (flat_epl<T>() + 1)];  // +1: conflict-free column reads
+};
+
+// Segmented inclusive scan of (flag, acc) pairs across the lanes (DPP steps
+// of wave_inclusive_scan): a flagged lane restarts the fold.
+template <class Acc>
+__device__ __forceinline__ void flat_seg_scan(bool &f, typename Acc::A &v)
+{
+    using A = typename Acc::A;
+    const A id = Acc::identity();
+    auto step = [&](int fu, A vu) {
+        v = f ? v : Acc::combine(vu, v);
+        f = f || fu != 0;
+    };
+    step(dpp_move<kDppRowShr + 1>((int)f, 0), Acc::template dpp_mv<kDppRowShr + 1, 0xF>(v, id));
+    step(dpp_move<kDppRowShr + 2>((int)f, 0), Acc::template dpp_mv<kDppRowShr + 2, 0xF>(v, id));
+    step(dpp_move<kDppRowShr + 4>((int)f, 0), Acc::template dpp_mv<kDppRowShr + 4, 0xF>(v, id));
+    step(dpp_move<kDppRowShr + 8>((int)f, 0), Acc::template dpp_mv<kDppRowShr + 8, 0xF>(v, id));
+    step(dpp_move<kDppRowBcast15, 0xA>((int)f, 0), Acc::template dpp_mv<kDppRowBcast15, 0xA>(v, id));
+    step(dpp_move<kDppRowBcast31, 0xC>((int)f, 0), Acc::template dpp_mv<kDppRowBcast31, 0xC>(v, id));
+}
+
+template <class T, int OP>
+__device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__restrict__ out,
+                                              uint32_t *__restrict__ index_out, T init, uint64_t wseg0,
+                                              uint32_t nvalid, uint32_t b, uint32_t len, uint32_t *bnd,
+                                              T *stage)
+{
+    using Acc = SegAcc<T, OP>;
+    using A = typename Acc::A;
+    constexpr int EPL = flat_epl<T>();
+    constexpr int VEC = 16 / (int)sizeof(T);
+    constexpr int LOADS = EPL / VEC;
+    constexpr uint32_t CH = kWave * EPL;
+    const uint32_t lane = lane_id();
+    const bool valid = lane < nvalid;
+    const uint32_t B = (uint32_t)__builtin_amdgcn_readfirstlane((int)b);
+    const uint32_t E = (uint32_t)__builtin_amdgcn_readlane((int)(b + len), (int)nvalid - 1);
+    bnd[lane] = valid ? b : E;
+    if (lane == 0) bnd[kSegPerWave] = E;
+    __builtin_amdgcn_wave_barrier();
+    if (valid && len == 0) seg_store<T, OP>(Acc::identity(), b, init, out, index_out, wseg0 + lane);
+    const uint32_t A0 = B & ~(uint32_t)(VEC - 1);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(in + A0, (E - A0) * (uint32_t)sizeof(T));  // reads past E give 0
+    const uint32_t nch = (E - A0 + CH - 1) / CH;
+    auto emit = [&](uint32_t sid, A acc) { seg_store<T, OP>(acc, bnd[sid], init, out, index_out, wseg0 + sid); };
+    A carry = Acc::identity();
+    // coalesced loads of chunk c: lane l, load k -> elements k*64*VEC + l*VEC .. + VEC - 1
+    u32x4 v[LOADS];
+    auto load_chunk = [&](uint32_t c) {
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k)
+            v[k] = buf_ld16_nt(r, (c * CH + (uint32_t)k * kWave * VEC + lane * VEC) * (uint32_t)sizeof(T), 0);
+    };
+    if (nch) load_chunk(0);
+#pragma unroll 1
+    for (uint32_t c = 0; c < nch; ++c) {
+        const uint32_t base = A0 + c * CH;  // element index of the chunk's first element
+        // chunk element q = k*64*VEC + lane*VEC + j belongs to lane q / EPL, position q % EPL
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) {
+            T e[VEC];
+            unpack16<T>(v[k], e);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                const uint32_t q = (uint32_t)k * kWave * VEC + lane * VEC + (uint32_t)j;
+                stage[(q / EPL) * (EPL + 1) + q % EPL] = e[j];
+            }
+        }
+        if (c + 1 < nch) load_chunk(c + 1);  // in flight while this chunk is folded
+        __builtin_amdgcn_wave_barrier();
+        T x[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) x[j] = stage[lane * (EPL + 1) + j];
+        __builtin_amdgcn_wave_barrier();
+
+        // the segment holding element p0 - 1: the last boundary below p0
+        const uint32_t p0 = base + lane * EPL;
+        uint32_t lo = 0, hi = kSegPerWave + 1;  // lo = number of boundaries below p0
+#pragma unroll
+        for (int it = 0; it < 7; ++it) {
+            if (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (bnd[mid] < p0) lo = mid + 1;
+                else hi = mid;
+            }
+        }
+        uint32_t sid = lo > 0 ? (lo - 1 < kSegPerWave ? lo - 1 : kSegPerWave - 1) : 0u;
+        uint32_t nb = bnd[sid + 1];
+        A acc = Acc::identity(), first_acc = Acc::identity();
+        uint32_t first_sid = 0;
+        bool seen = false;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const uint32_t p = p0 + (uint32_t)j;
+            if (p >= B && p < E) {
+                if (p == nb) {  // segment sid ended at p - 1
+                    if (!seen) {
+                        first_sid = sid;
+                        first_acc = acc;
+                        seen = true;
+                    } else {
+                        emit(sid, acc);
+                    }
+                    do {  // skip the empty segments that start and end at p
+                        ++sid;
+                        nb = bnd[sid + 1];
+                    } while (nb == p);
+                    acc = Acc::identity();
+                }
+                acc = Acc::fold(acc, x[j], p);
+            }
+        }
+        // open segment at each lane's start: carry, then the lanes before
+        bool f = seen;
+        A inc = acc;
+        flat_seg_scan<Acc>(f, inc);
+        const int fprev = wave_shr1((int)f, 0);
+        const A iprev = Acc::template dpp_mv<kDppWaveShr1, 0xF>(inc, Acc::identity());
+        const A open = lane == 0 ? carry : (fprev ? iprev : Acc::combine(carry, iprev));
+        if (seen) emit(first_sid, Acc::combine(open, first_acc));
+        const bool f63 = __builtin_amdgcn_readlane((int)f, kWave - 1) != 0;
+        const A i63 = Acc::readlane_acc(inc, kWave - 1);
+        carry = f63 ? i63 : Acc::combine(carry, i63);
+    }
+    // the range's last non-empty segment ends at E
+    const uint64_t ne = ballot(valid && len > 0);
+    if (ne && lane == 0) emit(63u - (uint32_t)__builtin_clzll(ne), carry);
+}
+
 template <class T, int OP, bool FIXED>
 __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__restrict__ in, T *__restrict__ out,
                                                                    uint32_t *__restrict__ index_out, uint64_t S,
-                                                                   SegBounds sb, T init)
+                                                                   SegBounds sb, T init, int vec_ok)
 {
     using Acc = SegAcc<T, OP>;
     using A = typename Acc::A;
@@ -213,6 +378,7 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__re
     __shared__ uint32_t s_long[kBatch];
     __shared__ uint32_t s_nlong;
     __shared__ A s_wave[kSegWaves];
+    __shared__ FlatSmem<T> s_flat;
 
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
     const uint64_t wseg0 = (uint64_t)blockIdx.x * kBatch + (uint64_t)wave * kSegPerWave;
@@ -224,6 +390,13 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__re
     const bool is_long = len > kSegLong;
     if (is_long) s_long[atomicAdd(&s_nlong, 1u)] = (uint32_t)(wave * kSegPerWave + lane);
 
+    // flat path when the wave's segments tile one range and none is long
+    const uint32_t nvalid = wseg0 < S ? (uint32_t)(S - wseg0 < kSegPerWave ? S - wseg0 : kSegPerWave) : 0u;
+    const uint32_t b_next = (uint32_t)__shfl_down((int)b, 1);
+    const bool breaks = lane < nvalid && (len > kSegLong || (lane + 1 < nvalid && b + len != b_next));
+    if (vec_ok && nvalid > 0 && ballot(breaks) == 0) {
+        flat_segments<T, OP>(in, out, index_out, init, wseg0, nvalid, b, len, s_flat.bnd[wave], s_flat.stage[wave]);
+    } else {
     A mine = Acc::identity();
 #pragma unroll 1
     for (int j0 = 0; j0 < kSegPerWave; j0 += kSegGroup) {
@@ -267,6 +440,7 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__re
     }
     if (lane < (uint32_t)kSegPerWave && wseg0 + lane < S && !is_long)
         seg_store<T, OP>(mine, b, init, out, index_out, wseg0 + lane);
+    }
 
     // ---- long segments: the whole workgroup streams each one
     __syncthreads();
@@ -342,8 +516,9 @@ int segment_launch(const void *in_, void *out_, uint32_t *index_out, uint64_t S,
     }
     const uint64_t blocks = ceil_div(S, (uint64_t)kSegWaves * kSegPerWave);
     const uint32_t grid = (uint32_t)blocks;
+    const int vec_ok = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
     LCPP_LAUNCH("segment_reduce", s,
-                (segment_reduce_kernel<T, OP, FIXED><<<grid, kSegBlock, 0, s>>>(in, out, index_out, S, sb, init)));
+                (segment_reduce_kernel<T, OP, FIXED><<<grid, kSegBlock, 0, s>>>(in, out, index_out, S, sb, init, vec_ok)));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
 }

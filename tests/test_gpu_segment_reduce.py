@@ -225,3 +225,72 @@ def test_arg_infinite_and_all_equal(gpu):
     assert list(i) == [1, 1, 2, 1] and v[0] == -np.inf and v[1] == np.inf and v[3] == np.finfo(np.float32).min
     v, i = seg_call("ArgMin", d, 4, (b, e), np.float32, arg=True)
     assert list(i) == [0, 0, 0, 1] and v[3] == np.finfo(np.float32).max
+
+
+def contiguous_layout(lengths):
+    """CSR begin/end offsets of segments that tile [0, sum(lengths)) in order."""
+    L = np.asarray(lengths, dtype=np.int64)
+    e = np.cumsum(L)
+    b = e - L
+    return b.astype(np.uint32), e.astype(np.uint32)
+
+
+# Segments that tile one range take the flat path of a wave (64 segments):
+# chunk-sized, lane-sized and single-element segments, empty segments at the
+# start, middle and end of a wave, a wave of empty segments only, the longest
+# flat segment (8192) and a long one (8193, whose wave falls back).
+FLAT_LAYOUTS = {
+    "lane_and_chunk": [16, 1024, 1, 15, 17, 1023, 1025, 512, 513, 2, 3, 4] * 11,
+    "empty_edges": [0, 0, 5, 0, 0, 130, 0, 7, 0, 0] * 13 + [0] * 70 + [9, 0, 0],
+    "all_empty_wave": [3] * 64 + [0] * 64 + [4] * 70,
+    "max_flat_and_long": [8192, 1, 8192, 0, 100] + [70] * 59 + [8193, 5, 0, 6] + [128] * 60,
+}
+
+
+@pytest.mark.parametrize("layout", sorted(FLAT_LAYOUTS))
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("pad", [0, 1])
+def test_contiguous_layouts_sum(gpu, layout, dtype, pad):
+    import gpu_util as g
+
+    b, e = contiguous_layout(FLAT_LAYOUTS[layout])
+    n = int(e[-1])
+    a = g.random_array(dtype, n, seed=n + pad)
+    log(f"segment contiguous {layout} {np.dtype(dtype).name} pad={pad}")
+    d = g.to_dev(a, pad=pad)  # pad = 1: misaligned input takes the segment-walking path
+    assert (run(d, b, e, dtype) == o.segment_reduce(o.OP_SUM, a, b, e)).all()
+
+
+@pytest.mark.parametrize("layout", sorted(FLAT_LAYOUTS))
+@pytest.mark.parametrize("dtype", [np.int32, np.float32, np.uint64, np.float64])
+def test_contiguous_layouts_min_max_arg(gpu, layout, dtype):
+    import gpu_util as g
+
+    b, e = contiguous_layout(FLAT_LAYOUTS[layout])
+    n = int(e[-1])
+    rng = np.random.default_rng(n)
+    a = rng.integers(0, 40, n).astype(dtype)  # ties
+    d = g.to_dev(a)
+    S = b.size
+    log(f"segment contiguous min/max/arg {layout} {np.dtype(dtype).name}")
+    for method, op in (("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        assert same(seg_call(method, d, S, (b, e), dtype), o.segment_reduce(op, a, b, e))
+    for method, is_max in (("ArgMin", False), ("ArgMax", True)):
+        v, i = seg_call(method, d, S, (b, e), dtype, arg=True)
+        ev, ei = o.segment_reduce_arg(is_max, a, b, e)
+        assert same(v, ev) and (i == ei).all()
+
+
+def test_contiguous_then_scattered_waves(gpu):
+    """Waves of one launch take different paths: tiling waves, then waves with
+    gaps and overlaps."""
+    import gpu_util as g
+
+    rng = np.random.default_rng(77)
+    b1, e1 = contiguous_layout(rng.geometric(1 / 100, 256 * 3) - 1)
+    n = int(e1[-1]) + 50_000
+    b2 = rng.integers(0, n - 300, 256 * 2).astype(np.uint32)
+    e2 = (b2 + rng.integers(0, 300, b2.size)).astype(np.uint32)
+    b, e = np.concatenate([b1, b2]), np.concatenate([e1, e2])
+    a = g.random_array(np.int32, n, seed=5)
+    assert (run(g.to_dev(a), b, e, np.int32) == o.segment_reduce(o.OP_SUM, a, b, e)).all()
