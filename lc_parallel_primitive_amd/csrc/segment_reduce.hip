@@ -53,9 +53,11 @@ constexpr int kSegWaves = kSegBlock / kWave;
 // grid of waves striding over groups of 8 measured 141-190 us, and 16-byte
 // vector loads with index masking 127 us (fewer waves fit).  The per-segment
 // wave reductions use DPP and readlane instead of __shfl_xor (ds_bpermute
-// through LDS): 119-122 -> 113 us.  The flat path takes C5 to 104-105 us (a
-// copy of it that only sums each wave's range, with no segment logic, runs
-// in 87.5 us).
+// through LDS): 119-122 -> 113 us.  The flat path takes C5 to 97 us (a copy
+// of it that only sums each wave's range, with no segment logic, runs in
+// 87.5 us): per-element branches 105 us, branch-free fold 99 us, segment of
+// each lane's first element by a 7-step binary search in LDS 99 us against
+// a slot histogram and a DPP scan 97 us.
 constexpr int kSegGroup = 8;
 constexpr int kSegPerWave = 64;
 constexpr uint32_t kSegLong = 8192;
@@ -237,6 +239,7 @@ constexpr int flat_epl()
 template <class T>
 struct FlatSmem {
     uint32_t bnd[kSegWaves][kSegPerWave + 1];
+    uint32_t slots[kSegWaves][kWave];
     T stage[kSegWaves][kWave * (flat_epl<T>() + 1)];  // +1: conflict-free column reads
 };
 
@@ -263,7 +266,7 @@ template <class T, int OP>
 __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__restrict__ out,
                                               uint32_t *__restrict__ index_out, T init, uint64_t wseg0,
                                               uint32_t nvalid, uint32_t b, uint32_t len, uint32_t *bnd,
-                                              T *stage)
+                                              uint32_t *slots, T *stage)
 {
     using Acc = SegAcc<T, OP>;
     using A = typename Acc::A;
@@ -313,41 +316,96 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
         for (int j = 0; j < EPL; ++j) x[j] = stage[lane * (EPL + 1) + j];
         __builtin_amdgcn_wave_barrier();
 
-        // the segment holding element p0 - 1: the last boundary below p0
+        // the segment holding element p0 - 1 is the last boundary below p0.
+        // Boundaries are counted per lane: boundary i (lane i's) is below
+        // the first element of every lane after slot (b_i - base) / EPL, so
+        // the count is a prefix sum of a 64-entry histogram of slots (those
+        // below the chunk counted by one ballot).
         const uint32_t p0 = base + lane * EPL;
-        uint32_t lo = 0, hi = kSegPerWave + 1;  // lo = number of boundaries below p0
-#pragma unroll
-        for (int it = 0; it < 7; ++it) {
-            if (lo < hi) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (bnd[mid] < p0) lo = mid + 1;
-                else hi = mid;
-            }
-        }
-        uint32_t sid = lo > 0 ? (lo - 1 < kSegPerWave ? lo - 1 : kSegPerWave - 1) : 0u;
-        uint32_t nb = bnd[sid + 1];
+        const uint32_t bi = valid ? b : E;
+        const uint32_t below = (uint32_t)__builtin_popcountll(ballot(bi < base));
+        slots[lane] = 0;
+        __builtin_amdgcn_wave_barrier();
+        if (bi >= base && bi - base < CH - EPL) atomicAdd(&slots[(bi - base) / EPL + 1], 1u);
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t cnt = below + wave_inclusive_scan(slots[lane], SumOp());
+        uint32_t sid = cnt > 0 ? (cnt - 1 < kSegPerWave ? cnt - 1 : kSegPerWave - 1) : 0u;
         A acc = Acc::identity(), first_acc = Acc::identity();
         uint32_t first_sid = 0;
         bool seen = false;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            const uint32_t p = p0 + (uint32_t)j;
-            if (p >= B && p < E) {
-                if (p == nb) {  // segment sid ended at p - 1
-                    if (!seen) {
-                        first_sid = sid;
-                        first_acc = acc;
-                        seen = true;
-                    } else {
-                        emit(sid, acc);
-                    }
-                    do {  // skip the empty segments that start and end at p
-                        ++sid;
-                        nb = bnd[sid + 1];
-                    } while (nb == p);
-                    acc = Acc::identity();
+        if constexpr (!Acc::kArg) {
+            // branch-free: bit t of hmask = a segment starts at p0 + t; fold
+            // with restarts, values back into this lane's LDS row
+            const uint32_t lim = p0 + EPL < E ? p0 + EPL : E;
+            uint32_t hmask = 0;
+            {
+                uint32_t i = sid + 1, q = bnd[i];
+                while (q < lim) {
+                    hmask |= 1u << (q - p0);
+                    q = bnd[++i];
                 }
-                acc = Acc::fold(acc, x[j], p);
+            }
+            const uint32_t vlo = B > p0 ? B - p0 : 0u;
+            const uint32_t vhi = lim > p0 ? lim - p0 : 0u;
+            A v = Acc::identity();
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                const A xj = (uint32_t)j >= vlo && (uint32_t)j < vhi ? A(x[j]) : Acc::identity();
+                v = ((hmask >> j) & 1u) ? xj : Acc::combine(v, xj);
+                x[j] = v;
+            }
+            acc = v;
+            seen = hmask != 0;
+            if (__builtin_amdgcn_ballot_w64(seen)) {
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) stage[lane * (EPL + 1) + j] = x[j];
+                __builtin_amdgcn_wave_barrier();
+                if (seen) {
+                    // walk the boundaries again: the segment before each one
+                    // ends at t - 1; the first of them may have started in
+                    // earlier lanes (written after the scan below)
+                    uint32_t prev = sid, i = sid + 1, q = bnd[i];
+                    bool first = true;
+                    while (q < lim) {
+                        uint32_t q2 = bnd[i + 1];
+                        while (q2 == q) q2 = bnd[++i + 1];  // empty segments starting at q
+                        const uint32_t t = q - p0;
+                        const A val = t ? A(stage[lane * (EPL + 1) + t - 1]) : Acc::identity();
+                        if (first) {
+                            first_sid = prev;
+                            first_acc = val;
+                            first = false;
+                        } else {
+                            emit(prev, val);
+                        }
+                        prev = i++;
+                        q = q2;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        } else {
+            uint32_t nb = bnd[sid + 1];
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                const uint32_t p = p0 + (uint32_t)j;
+                if (p >= B && p < E) {
+                    if (p == nb) {  // segment sid ended at p - 1
+                        if (!seen) {
+                            first_sid = sid;
+                            first_acc = acc;
+                            seen = true;
+                        } else {
+                            emit(sid, acc);
+                        }
+                        do {  // skip the empty segments that start and end at p
+                            ++sid;
+                            nb = bnd[sid + 1];
+                        } while (nb == p);
+                        acc = Acc::identity();
+                    }
+                    acc = Acc::fold(acc, x[j], p);
+                }
             }
         }
         // open segment at each lane's start: carry, then the lanes before
@@ -395,7 +453,8 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__re
     const uint32_t b_next = (uint32_t)__shfl_down((int)b, 1);
     const bool breaks = lane < nvalid && (len > kSegLong || (lane + 1 < nvalid && b + len != b_next));
     if (vec_ok && nvalid > 0 && ballot(breaks) == 0) {
-        flat_segments<T, OP>(in, out, index_out, init, wseg0, nvalid, b, len, s_flat.bnd[wave], s_flat.stage[wave]);
+        flat_segments<T, OP>(in, out, index_out, init, wseg0, nvalid, b, len, s_flat.bnd[wave], s_flat.slots[wave],
+                             s_flat.stage[wave]);
     } else {
     A mine = Acc::identity();
 #pragma unroll 1
