@@ -103,17 +103,6 @@ struct SegAcc {
         if constexpr (kArg) return combine(a, A{x, i});
         else return combine(a, x);
     }
-    static __device__ __forceinline__ A shfl_xor_acc(A a, int m)
-    {
-        if constexpr (kArg) {
-            A r;
-            r.value = shfl_xor(a.value, m);
-            r.index = (uint32_t)__shfl_xor((int)a.index, m);
-            return r;
-        } else {
-            return shfl_xor(a, m);
-        }
-    }
     // DPP inside rows of 16, then the four row results (wave-uniform)
     template <int CTRL>
     static __device__ __forceinline__ A dpp_acc(A a)
