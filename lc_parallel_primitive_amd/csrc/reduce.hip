@@ -6,13 +6,14 @@
 // block/detail/block_reduce_warp.h:29-70, warp/details/warp_reduce_shlf.h,
 // common/thread_operators.h:19-47 (ArgMaxOp/ArgMinOp).
 //
-// MI355X design: one streaming pass.  A grid of at most 2048 workgroups
-// (256 CUs x 8) partitions the input into equal contiguous chunks whose
-// length is a multiple of the 16 KiB tile, so every workgroup's range is
-// exact (the reference dispatches more blocks than it partitions for
-// N > 10,485,760 and reads past the end).  Each thread streams 16-byte
-// vectors (8 in flight), folds them in registers, the workgroup folds its
-// four wave totals, and one partial per workgroup lands in temp storage.  A
+// MI355X design: one streaming pass.  A grid of at most 512 workgroups
+// (2048 for ArgMin/ArgMax) partitions the input into equal contiguous chunks
+// whose length is a multiple of the tile (128 KiB; 32 KiB for Arg*), so
+// every workgroup's range is exact (the reference dispatches more blocks
+// than it partitions for N > 10,485,760 and reads past the end).  Each thread
+// streams 16-byte vectors (32 per tile; 8 for Arg*), folds them in
+// registers, the workgroup folds its four wave totals, and one partial per
+// workgroup lands in temp storage.  A
 // one-workgroup kernel folds the partials in a fixed order, so the float
 // result is deterministic for a given N.  N <= one tile needs no temp and
 // one launch.
@@ -28,13 +29,26 @@ namespace lcpp {
 namespace {
 
 constexpr int kRedBlock = 256;
-constexpr int kRedVecs = 8;            // 16-byte vectors per thread per tile
-constexpr uint32_t kRedMaxGrid = 2048; // 256 CUs x 8 workgroups
+// Geometry (16-byte vectors per thread per tile, most workgroups), measured
+// at 2^28 int32 (us, Sum / ArgMin): 2048 x 8: 158 / 163; 1024 x 16: 154;
+// 512 x 16: 152 / 181; 512 x 32: 150 / 177; 256 x 32: 186 / 289; 512 x 48:
+// 154 / 191.  Plain folds take 512 workgroups of 32 vectors (two per CU,
+// each streaming 2 MiB); the (value, index) folds keep 2048 x 8.
+template <bool ARG>
+constexpr int red_vecs()
+{
+    return ARG ? 8 : 32;
+}
+template <bool ARG>
+constexpr uint32_t red_max_grid()
+{
+    return ARG ? 2048 : 512;
+}
 
-template <class T>
+template <class T, bool ARG>
 constexpr uint64_t red_tile()
 {
-    return (uint64_t)kRedBlock * kRedVecs * (16 / sizeof(T));
+    return (uint64_t)kRedBlock * red_vecs<ARG>() * (16 / sizeof(T));
 }
 
 struct RedGrid {
@@ -42,13 +56,13 @@ struct RedGrid {
     uint64_t chunk;  // elements per workgroup, multiple of the tile
 };
 
-template <class T>
+template <class T, bool ARG>
 RedGrid red_grid(uint64_t n)
 {
-    const uint64_t tile = red_tile<T>();
+    const uint64_t tile = red_tile<T, ARG>();
     uint64_t tiles = ceil_div(n, tile);
     if (tiles == 0) tiles = 1;
-    uint64_t grid = tiles < kRedMaxGrid ? tiles : kRedMaxGrid;
+    uint64_t grid = tiles < red_max_grid<ARG>() ? tiles : red_max_grid<ARG>();
     uint64_t chunk = ceil_div(tiles, grid) * tile;
     grid = n ? ceil_div(n, chunk) : 1;
     return {(uint32_t)grid, chunk};
@@ -168,17 +182,18 @@ __global__ __launch_bounds__(kRedBlock) void reduce_partials_kernel(const T *__r
     const uint64_t b1 = b0 + chunk < n ? b0 + chunk : n;
     const uint32_t tid = threadIdx.x;
     constexpr uint64_t V = 16 / sizeof(T);
-    constexpr uint64_t tile = red_tile<T>();
+    constexpr uint64_t tile = red_tile<T, false>();
+    constexpr int VECS = red_vecs<false>();
     uint64_t tail = b0;
     if ((reinterpret_cast<uintptr_t>(in) & 15) == 0) {
         const uint64_t full_end = b0 + (b1 - b0) / tile * tile;
         for (uint64_t t = b0; t < full_end; t += tile) {
-            u32x4 v[kRedVecs];
+            u32x4 v[VECS];
 #pragma unroll
-            for (int i = 0; i < kRedVecs; ++i)
+            for (int i = 0; i < VECS; ++i)
                 v[i] = ld16_nt((in + t + ((uint64_t)i * kRedBlock + tid) * V));
 #pragma unroll
-            for (int i = 0; i < kRedVecs; ++i) acc = fold16<T>(acc, v[i], op, xf);
+            for (int i = 0; i < VECS; ++i) acc = fold16<T>(acc, v[i], op, xf);
         }
         tail = full_end;
     }
@@ -202,7 +217,7 @@ __global__ __launch_bounds__(kRedBlock) void reduce_final_kernel(const T *__rest
 template <class T>
 uint64_t reduce_temp(uint64_t n)
 {
-    RedGrid g = red_grid<T>(n);
+    RedGrid g = red_grid<T, false>(n);
     return g.grid > 1 ? align_up((uint64_t)g.grid * sizeof(T), 256) : 0;
 }
 
@@ -213,7 +228,7 @@ int reduce_launch(void *temp, size_t temp_bytes, const void *in_, void *out_, ui
     const T *in = static_cast<const T *>(in_);
     T *out = static_cast<T *>(out_);
     if (!out || (n && !in)) return LCPP_ERR_INVALID_ARG;
-    RedGrid g = red_grid<T>(n);
+    RedGrid g = red_grid<T, false>(n);
     if (g.grid == 1) {
         // one workgroup writes op(init, fold) itself
         if (n == 0) {
@@ -268,17 +283,18 @@ __global__ __launch_bounds__(kRedBlock) void arg_partials_kernel(const T *__rest
     const uint64_t b1 = b0 + chunk < n ? b0 + chunk : n;
     const uint32_t tid = threadIdx.x;
     constexpr uint64_t V = 16 / sizeof(T);
-    constexpr uint64_t tile = red_tile<T>();
+    constexpr uint64_t tile = red_tile<T, true>();
+    constexpr int VECS = red_vecs<true>();
     uint64_t tail = b0;
     if ((reinterpret_cast<uintptr_t>(in) & 15) == 0) {
         const uint64_t full_end = b0 + (b1 - b0) / tile * tile;
         for (uint64_t t = b0; t < full_end; t += tile) {
-            u32x4 v[kRedVecs];
+            u32x4 v[VECS];
 #pragma unroll
-            for (int i = 0; i < kRedVecs; ++i)
+            for (int i = 0; i < VECS; ++i)
                 v[i] = ld16_nt((in + t + ((uint64_t)i * kRedBlock + tid) * V));
 #pragma unroll
-            for (int i = 0; i < kRedVecs; ++i) {
+            for (int i = 0; i < VECS; ++i) {
                 T e[V];
                 unpack16<T>(v[i], e);
                 const uint32_t i0 = (uint32_t)(t + ((uint64_t)i * kRedBlock + tid) * V);
@@ -319,7 +335,7 @@ __global__ __launch_bounds__(kRedBlock) void arg_final_kernel(const IdxVal<T> *_
 template <class T>
 uint64_t arg_temp(uint64_t n)
 {
-    RedGrid g = red_grid<T>(n);
+    RedGrid g = red_grid<T, true>(n);
     return g.grid > 1 ? align_up((uint64_t)g.grid * sizeof(IdxVal<T>), 256) : 0;
 }
 
@@ -331,7 +347,7 @@ int arg_launch(void *temp, size_t temp_bytes, const void *in_, void *out_, uint3
     T *out = static_cast<T *>(out_);
     if (!out || !out_index || (n && !in)) return LCPP_ERR_INVALID_ARG;
     if (n > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;  // 32-bit indices, as the reference
-    RedGrid g = red_grid<T>(n);
+    RedGrid g = red_grid<T, true>(n);
     if (g.grid == 1) {
         if (n == 0) {
             LCPP_LAUNCH("arg_final", s, (arg_final_kernel<T, IS_MAX><<<1, kRedBlock, 0, s>>>(nullptr, 0, out, out_index)));

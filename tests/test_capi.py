@@ -60,10 +60,12 @@ def test_temp_bytes_queries(L):
     # reduce: one partial per workgroup (<= 2048), none when one workgroup suffices
     assert _q(L.lcpp_reduce_temp_bytes, 0, 0) == (0, 0)
     assert _q(L.lcpp_reduce_temp_bytes, 0, 8192) == (0, 0)
-    rc, b = _q(L.lcpp_reduce_temp_bytes, 0, 1 << 28)
-    assert rc == 0 and b == 2048 * 4
+    rc, b = _q(L.lcpp_reduce_temp_bytes, 0, 1 << 28)  # one partial per workgroup, at most 512
+    assert rc == 0 and b == 512 * 4
     rc, b = _q(L.lcpp_reduce_temp_bytes, 5, 1 << 28)
-    assert rc == 0 and b == 2048 * 8
+    assert rc == 0 and b == 512 * 8
+    assert _q(L.lcpp_reduce_temp_bytes, 0, 32768) == (0, 0)  # one 128 KiB tile: one workgroup, no temp
+    assert _q(L.lcpp_reduce_temp_bytes, 0, 32769) == (0, 256)
     # arg reduce: one (value, index) partial per workgroup
     rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 2, 1 << 28)
     assert rc == 0 and b == 2048 * 8

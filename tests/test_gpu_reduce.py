@@ -47,8 +47,10 @@ def test_kat_min_max_shuffled(gpu):
     assert run("Sum", d, a.size, np.int32) == exp[2]
 
 
+# tiles hold 32768 4-byte / 16384 8-byte elements (8192 / 4096 for Arg*); at
+# 20M elements the grid is at its 512-workgroup cap with a ragged last chunk
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("n", [1, 63, 4097, 32768, 1_000_003])
+@pytest.mark.parametrize("n", [1, 63, 4097, 16384, 16385, 32768, 32769, 1_000_003, 20_000_003])
 @pytest.mark.parametrize("pad", [0, 1])
 def test_all_dtypes_vs_oracle(gpu, dtype, n, pad):
     import gpu_util as g
