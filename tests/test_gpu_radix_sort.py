@@ -265,3 +265,24 @@ def test_constant_keys_all_lanes_hot(gpu):
     v = np.arange(n, dtype=np.uint32)
     ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, np.uint32, np.uint32)
     assert (g.to_host(ko) == 7).all() and (g.to_host(vo) == v).all()
+
+
+# Digit passes in which every key has the same digit are skipped; these masks
+# leave trivial passes at the start, in the middle and at the end, and one
+# pass or several that move data (the pass plan's buffer ping-pong).
+@pytest.mark.parametrize("kdt,mask", [(np.uint32, 0x0000FF00), (np.uint32, 0xFF00FF00), (np.uint32, 0x00FF0000),
+                                      (np.uint32, 0xFF000000), (np.uint32, 0x00FFFF00), (np.uint64, 0x00FF00FF00FF00FF),
+                                      (np.uint64, 0xFF00000000000000), (np.uint64, 0x0000FFFF00000000)])
+@pytest.mark.parametrize("descending", [False, True])
+def test_trivial_passes_skipped(gpu, kdt, mask, descending):
+    import gpu_util as g
+
+    n = 300_007
+    k = g.random_array(kdt, n, seed=11) & np.array(mask, dtype=kdt)
+    v = np.arange(n, dtype=np.uint32)
+    log(f"sort trivial passes {np.dtype(kdt).name} mask={mask:#x} descending={descending}")
+    got = g.to_host(sort_keys(g.to_dev(k), n, kdt, descending=descending))
+    assert same_bits(got, o.radix_sort(k, descending=descending))
+    ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, kdt, np.uint32, descending=descending)
+    rk, rv = o.radix_sort(k, v, descending=descending)
+    assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
