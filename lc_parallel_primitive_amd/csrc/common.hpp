@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <limits>
 #include <type_traits>
 
@@ -340,6 +341,41 @@ struct LaunchScope {
     ~LaunchScope();
     void *rec;
 };
+
+// Host cache of per-device launch facts (CU count, occupancy, function
+// attributes): one slot per device ordinal, filled by the first call on that
+// device.  Racing first calls compute the same value, so relaxed atomics
+// suffice and concurrent callers never see a torn or foreign-device value.
+// `compute` runs with the device current and returns a non-zero value.
+constexpr int kMaxDevices = 64;
+struct DeviceCache {
+    std::atomic<int> v[kMaxDevices];
+};
+template <class F>
+int device_cached(DeviceCache &c, F compute)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return compute();
+    int x = c.v[dev].load(std::memory_order_relaxed);
+    if (x == 0) {
+        x = compute();
+        c.v[dev].store(x, std::memory_order_relaxed);
+    }
+    return x;
+}
+
+// Compute units of the current device (256 on MI355X; 256 if the query fails).
+inline int device_cus()
+{
+    static DeviceCache cache;
+    return device_cached(cache, [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            return cus;
+        return 256;
+    });
+}
 
 }  // namespace lcpp
 

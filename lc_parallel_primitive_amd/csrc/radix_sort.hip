@@ -664,20 +664,6 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     return L;
 }
 
-int num_cus()
-{
-    static int cached = 0;
-    if (!cached) {
-        int dev = 0, cus = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-            cached = cus;
-        else
-            cached = 256;
-    }
-    return cached;
-}
-
 template <class UK, class UV, int KIND, bool PAIRS>
 int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const void *vin_,
            void *vout_, uint64_t n, bool descending, hipStream_t s)
@@ -710,17 +696,18 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     LCPP_CHECK_LAUNCH();
     {
         // one 1024-thread workgroup per CU (128 KB of LDS each)
-        static bool lds_set = false;
         constexpr size_t lds = hist_lds_bytes<UK>();
-        if (!lds_set) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void *>(&rs_histogram_kernel<UK, KIND>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-                return LCPP_ERR_HIP;
-            lds_set = true;
-        }
+        static DeviceCache lds_set;
+        if (device_cached(lds_set, [] {
+                return hipFuncSetAttribute(reinterpret_cast<const void *>(&rs_histogram_kernel<UK, KIND>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess
+                           ? 1
+                           : -1;
+            }) < 0)
+            return LCPP_ERR_HIP;
         const uint64_t htile = (uint64_t)kHistBlock * 4 * (16 / sizeof(UK));
         const uint64_t htiles = ceil_div(n, htile);
-        const uint64_t cus = (uint64_t)num_cus();
+        const uint64_t cus = (uint64_t)device_cus();
         uint64_t grid = htiles < cus ? htiles : cus;
         const uint64_t chunk = ceil_div(htiles, grid) * htile;
         grid = ceil_div(n, chunk);
@@ -732,18 +719,20 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     LCPP_LAUNCH("rs_hot", s, rs_hot_kernel<<<1, 256, 0, s>>>(bins, (uint32_t)P, n, hot, plan));
     LCPP_CHECK_LAUNCH();
     // XCD run length: 8R <= half the onesweep workgroups resident at once
-    static uint32_t log_run = 0xFFFFFFFFu;
-    if (log_run == 0xFFFFFFFFu) {
+    static DeviceCache run_cache;  // log2(R) + 1, or -1 when the occupancy query fails
+    const int lr1 = device_cached(run_cache, [] {
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
                 &per_cu, reinterpret_cast<const void *>(&rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS>), kOsBlock,
                 0) != hipSuccess)
-            return LCPP_ERR_HIP;
-        const uint64_t resident = (uint64_t)(per_cu > 0 ? per_cu : 1) * (uint64_t)num_cus();
-        uint32_t lr = 0;
+            return -1;
+        const uint64_t resident = (uint64_t)(per_cu > 0 ? per_cu : 1) * (uint64_t)device_cus();
+        int lr = 0;
         while (lr < 4 && (8ull << (lr + 1)) * 2 <= resident) ++lr;
-        log_run = lr;
-    }
+        return lr + 1;
+    });
+    if (lr1 < 0) return LCPP_ERR_HIP;
+    const uint32_t log_run = (uint32_t)(lr1 - 1);
     // buffers and look-back regions per pass come from the device-side plan
     const RsBuffers<UK, UV> buf{kin, ktmp, kout, vin, vtmp, vout};
     const LbState regions{tc[0], bw[0], tc[1], bw[1]};

@@ -3,6 +3,7 @@
 // Reference: runtime/core.h:35-112 (lazy JIT compile + memo, lcpp_check).
 // Here every kernel is compiled ahead of time for gfx950, so there is no JIT
 // cache; the C ABI returns status codes instead of asserting.
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -23,7 +24,7 @@ struct Aggregate {
 };
 
 std::mutex g_mu;
-bool g_on = false;
+std::atomic<bool> g_on{false};  // read on every launch without the lock
 std::vector<Record> g_pending;
 std::vector<Aggregate> g_agg;
 
@@ -37,13 +38,13 @@ struct Open {
 
 LaunchScope::LaunchScope(const char *name, hipStream_t s) : rec(nullptr)
 {
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        if (!g_on) return;
-    }
+    if (!g_on.load(std::memory_order_relaxed)) return;
     Open *o = new Open{name, nullptr, nullptr, s};
-    if (hipEventCreate(&o->start) != hipSuccess || hipEventCreate(&o->stop) != hipSuccess ||
-        hipEventRecord(o->start, s) != hipSuccess) {
+    const bool ok = hipEventCreate(&o->start) == hipSuccess && hipEventCreate(&o->stop) == hipSuccess &&
+                    hipEventRecord(o->start, s) == hipSuccess;
+    if (!ok) {
+        if (o->start) (void)hipEventDestroy(o->start);
+        if (o->stop) (void)hipEventDestroy(o->stop);
         delete o;
         return;
     }
@@ -94,7 +95,7 @@ extern "C" int lcpp_profile_enable(int on)
     std::lock_guard<std::mutex> lk(g_mu);
     drop_pending_locked();
     g_agg.clear();
-    g_on = on != 0;
+    g_on.store(on != 0, std::memory_order_relaxed);
     return LCPP_OK;
 }
 

@@ -508,33 +508,19 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_wg_kernel(const T *_
     for (uint64_t s = blockIdx.x; s < S; s += gridDim.x) wg_reduce_segment<T, OP, true>(in, out, index_out, s, S, sb, init, s_wave);
 }
 
-int num_cus_cached()
-{
-    static int cached = 0;
-    if (!cached) {
-        int dev = 0, cus = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-            cached = cus;
-        else
-            cached = 256;
-    }
-    return cached;
-}
-
-// Workgroups of `kernel` the device holds at once (cached per kernel).
+// Workgroups of `kernel` the current device holds at once (cached per kernel
+// and device).
 template <class K>
-int resident_blocks(K kernel, int &cache)
+int resident_blocks(K kernel, DeviceCache &cache)
 {
-    if (!cache) {
+    return device_cached(cache, [kernel] {
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kernel), kSegBlock, 0) !=
                 hipSuccess ||
             per_cu <= 0)
             per_cu = 4;
-        cache = per_cu * num_cus_cached();
-    }
-    return cache;
+        return per_cu * device_cus();
+    });
 }
 
 template <class T, int OP, bool FIXED>
@@ -554,7 +540,7 @@ int segment_launch(const void *in_, void *out_, uint32_t *index_out, uint64_t S,
         if (init_) memcpy(&init, init_, sizeof(T));
     }
     if (FIXED && sb.size > kSegLong) {
-        static int cap = 0;
+        static DeviceCache cap;
         const uint64_t c = (uint64_t)resident_blocks(&segment_reduce_wg_kernel<T, OP>, cap);
         const uint32_t grid = (uint32_t)(S < c ? S : c);
         LCPP_LAUNCH("segment_reduce_wg", s,
