@@ -95,8 +95,11 @@ __device__ __forceinline__ uint32_t bk_elem(int k, uint32_t t, int j)
 
 // Loads one tile.  `fast`: full tile and 16-byte aligned pointers; otherwise
 // element-wise raw-buffer loads whose offsets (all in the VGPR operand) are
-// range-checked against `valid` elements, returning 0 past it.
-template <class K, class V>
+// range-checked against `valid` elements, returning 0 past it.  KEYS_FIRST
+// issues every key load before the value loads, so that work on the keys
+// alone can start while the values are still in flight (loads complete in
+// issue order).
+template <bool KEYS_FIRST = false, class K, class V>
 __device__ __forceinline__ void bk_load(BkRegs<K, V> &r, const K *keys, const V *vals, uint64_t base,
                                         uint32_t valid, bool fast, uint32_t tid)
 {
@@ -107,7 +110,7 @@ __device__ __forceinline__ void bk_load(BkRegs<K, V> &r, const K *keys, const V 
     if (fast) {
 #pragma unroll
         for (int k = 0; k < kBkVecs; ++k) {
-            unpack16<V>(buf_ld16_nt(rv, tid * 16 + (uint32_t)k * kBkBlock * 16, 0), r.val[k]);
+            if constexpr (!KEYS_FIRST) unpack16<V>(buf_ld16_nt(rv, tid * 16 + (uint32_t)k * kBkBlock * 16, 0), r.val[k]);
             const uint32_t ko = tid * KB + (uint32_t)k * kBkBlock * KB;
             if constexpr (KB == 16) {
                 unpack16<K>(buf_ld16_nt(rk, ko, 0), r.key[k]);
@@ -126,6 +129,11 @@ __device__ __forceinline__ void bk_load(BkRegs<K, V> &r, const K *keys, const V 
                 r.key[k][0] = __builtin_bit_cast(K, a);
                 r.key[k][1] = __builtin_bit_cast(K, b);
             }
+        }
+        if constexpr (KEYS_FIRST) {
+#pragma unroll
+            for (int k = 0; k < kBkVecs; ++k)
+                unpack16<V>(buf_ld16_nt(rv, tid * 16 + (uint32_t)k * kBkBlock * 16, 0), r.val[k]);
         }
     } else {
 #pragma unroll

@@ -11,7 +11,11 @@
 // side by side in two waves of each tile: the number of heads before the
 // tile (a plain sum scan over tiles, it fixes the output index of every run)
 // and the fold of the open run entering the tile (a segmented scan: a tile
-// that contains a head publishes INCLUSIVE at once).  A head at element
+// that contains a head publishes INCLUSIVE at once).  The key loads are
+// issued before the value loads, and the tile's head count is published as
+// soon as the keys are in, while the values are still arriving: the count
+// chain is the longer wait (2^28 int32 keys, f32 values, runs of mean 128:
+// 531-546 -> 495-500 us per call).  A head at element
 // i > 0 closes the run that ends at i - 1 and writes its key and aggregate;
 // element n - 1 writes the last run and the run count, as the reference
 // does (reduce_by_key.h:231-254).  Consecutive runs land at consecutive
@@ -71,7 +75,7 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
     const bool fast = valid == TILE && vec_ok;
 
     BkRegs<K, V> r;
-    bk_load(r, keys, vin, base, valid, fast, tid);
+    bk_load<true>(r, keys, vin, base, valid, fast, tid);
     if (tid < kBkVecs) s_F[tid] = 0;
     K prev0[kBkVecs];
     const uint32_t fl = bk_heads<K, VP>(r.key, prev0, s_last, s_pred, keys, base, tile, tid);
@@ -82,10 +86,31 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
             for (int j = 0; j < VP; ++j) s_keys[bk_elem<V>(k, tid, j)] = r.key[k][j];
     }
 
-    // pass 1: per vector, (has-head, open fold) pairs and head counts, wave
-    // scans of both, wave totals to LDS
-    V exS[kBkVecs];
+    // head counts first (keys only; the values are still arriving): per
+    // vector a wave scan, wave totals to LDS, and the tile's count is
+    // published before the values are folded, so successors' count
+    // look-backs find it as early as possible
     uint32_t exC[kBkVecs];
+#pragma unroll
+    for (int k = 0; k < kBkVecs; ++k) {
+        const uint32_t c = (uint32_t)__builtin_popcount((fl >> (k * VP)) & ((1u << VP) - 1u));
+        const uint32_t ci = wave_inclusive_scan(c, SumOp());
+        exC[k] = ci - c;
+        if (lane == kWave - 1) s_C[k][wave] = ci;
+    }
+    __syncthreads();
+    uint32_t tcount = 0;
+    if (wave == 1) {
+#pragma unroll
+        for (int k = 0; k < kBkVecs; ++k)
+#pragma unroll
+            for (int w = 0; w < kBkWaves; ++w) tcount += s_C[k][w];
+        if (lane == 0) lb_publish(cwords, tile, tcount, tile == 0 ? kStInclusive : kStPartial);
+    }
+
+    // pass 1: per vector, (has-head, open fold) pairs, their wave scan, wave
+    // totals to LDS
+    V exS[kBkVecs];
     uint32_t exF = 0;
 #pragma unroll
     for (int k = 0; k < kBkVecs; ++k) {
@@ -99,18 +124,15 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
         const V su = shfl_up(s, 1);
         exS[k] = lane == 0 ? ident : su;
         exF |= (uint32_t)(lane != 0 && fu) << k;
-        const uint32_t c = (uint32_t)__builtin_popcount(bits);
-        const uint32_t ci = wave_inclusive_scan(c, SumOp());
-        exC[k] = ci - c;
         if (lane == kWave - 1) {
             s_S[k][wave] = s;
-            s_C[k][wave] = ci;
             if (f) atomicOr(&s_F[k], 1u << wave);
         }
     }
     __syncthreads();
 
-    // look-backs: wave 0 the open-run fold, wave 1 the head count
+    // look-backs: wave 0 the open-run fold, wave 1 the head count (its
+    // PARTIAL is already published)
     if (wave == 0) {
         bool tf = false;
         V ts = ident;
@@ -123,12 +145,11 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
         const V p = lb_segmented_tile(vwords, tile, ts, tf, true, op, ident);
         if (lane == 0) s_vprefix = p;
     } else if (wave == 1) {
-        uint32_t tc = 0;
-#pragma unroll
-        for (int k = 0; k < kBkVecs; ++k)
-#pragma unroll
-            for (int w = 0; w < kBkWaves; ++w) tc += s_C[k][w];
-        const uint32_t p = lb_scan_tile(cwords, tile, tc, SumOp(), 0u);
+        uint32_t p = 0;
+        if (tile > 0) {
+            p = lb_wait_prefix(cwords, tile, SumOp(), 0u);
+            if (lane == 0) lb_publish(cwords, tile, p + tcount, kStInclusive);
+        }
         if (lane == 0) s_cprefix = p;
     }
     __syncthreads();
