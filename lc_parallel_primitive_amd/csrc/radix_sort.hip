@@ -15,13 +15,15 @@
 // the pass needs, each tile would walk ~100 predecessors per digit.  The pass
 // here is built around that:
 //
-//  * launch 0 "rs_init": zero the P digit histograms.
+//  * launch 0 "rs_init": zero the P digit histograms and an arrival counter.
 //  * launch 1 "rs_histogram": one 1024-thread workgroup per CU streams a
 //    contiguous chunk of keys and counts all P = sizeof(K) 8-bit digits at
 //    once into an LDS table with 32 (16 for 8-byte keys) lane-private copies
 //    of every counter, so that equal digits in one wave (skewed or constant
 //    key bytes) never hit one LDS address; flushed with one global atomic per
-//    non-zero bin.  It also zeroes the look-back state of pass 0.
+//    non-zero bin.  It also zeroes the look-back state of pass 0.  The last
+//    workgroup to finish (the arrival counter) finds each pass's hot digit
+//    and plans the passes from the finished histograms (below).
 //  * launches 2..P+1 "rs_onesweep": one 16384-key tile (8192 for 8-byte keys
 //    or values) per 512-thread workgroup.  No ticket: tiles are mapped from
 //    the workgroup id so that every R consecutive tiles (R = 16 on a full
@@ -57,9 +59,9 @@
 //    instead of 64 KB), which lets keys-only passes run three workgroups per
 //    CU: consecutive threads write consecutive positions of each digit run.
 //    Values follow with the same ranks.
-//  * "rs_hot" also plans the passes on the device: a pass whose digit is the
-//    same for every key (from the histogram) is skipped, and the others
-//    ping-pong so that the last one writes the output.
+//  * The pass plan is made on the device: a pass whose digit is the same for
+//    every key (from the histogram) is skipped, and the others ping-pong so
+//    that the last one writes the output.
 //  * Descending order sorts the bit-inverted sort keys (one XOR in, one out),
 //    as RadixSortTwiddle<true> does; equal keys keep their input order.
 //  * Keys-only sorts reserve no value scratch (the reference reserves N
@@ -195,19 +197,20 @@ __global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *bins, uint32_t n
 constexpr uint32_t kPlanSkip = 1u, kPlanCopy = 2u;
 constexpr int kPlanSrcShift = 2, kPlanDstShift = 4, kPlanRegionShift = 6;
 enum PlanBuf : uint32_t { kBufIn = 0, kBufTmp = 1, kBufOut = 2 };
-__global__ __launch_bounds__(256) void rs_hot_kernel(const uint32_t *__restrict__ bins, uint32_t passes,
-                                                     uint64_t n, uint32_t *__restrict__ hot,
-                                                     uint32_t *__restrict__ plan)
+// Runs in the histogram's last workgroup (NT threads): the bins are read
+// with agent-scope loads, after every workgroup's adds have been counted.
+template <int NT>
+__device__ void rs_make_plan(const uint32_t *bins, uint32_t passes, uint64_t n, uint32_t *__restrict__ hot,
+                             uint32_t *__restrict__ plan, uint32_t *s_trivial)
 {
-    __shared__ uint32_t s_trivial[16];
     const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
-    for (uint32_t p = wave; p < passes; p += 256 / kWave) {
+    for (uint32_t p = wave; p < passes; p += NT / kWave) {
         // lane l looks at digits l, l + 64, l + 128, l + 192
         uint64_t best = 0;  // (count << 8) | (255 - digit): max picks the larger count, then the smaller digit
 #pragma unroll
         for (int q = 0; q < kRadix / kWave; ++q) {
             const uint32_t d = lane + (uint32_t)q * kWave;
-            const uint64_t c = ((uint64_t)bins[p * kRadix + d] << 8) | (255u - d);
+            const uint64_t c = ((uint64_t)ld_relaxed(&bins[p * kRadix + d]) << 8) | (255u - d);
             best = c > best ? c : best;
         }
 #pragma unroll
@@ -252,9 +255,9 @@ constexpr size_t hist_lds_bytes()
 
 template <class UK, int KIND>
 __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
-    const UK *__restrict__ keys, uint64_t n, uint64_t chunk, uint32_t *__restrict__ bins,
-    uint32_t *__restrict__ clear0, uint64_t clear0_words, uint32_t *__restrict__ clear1,
-    uint64_t clear1_words, UK flip)
+    const UK *__restrict__ keys, uint64_t n, uint64_t chunk, uint32_t *bins, uint32_t *__restrict__ clear0,
+    uint64_t clear0_words, uint32_t *__restrict__ clear1, uint64_t clear1_words, UK flip, uint32_t *arrivals,
+    uint32_t *__restrict__ hot, uint32_t *__restrict__ plan)
 {
     constexpr int P = sizeof(UK);
     constexpr int C = hist_copies<UK>();
@@ -294,16 +297,30 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     }
     for (uint64_t i = tail + tid; i < b1; i += kHistBlock) count(keys[i]);
     __syncthreads();
+    // global adds with their results consumed: each has been performed
+    // before this workgroup's arrival below is counted
+    uint32_t seen = 0;
     for (uint32_t i = tid; i < (uint32_t)(P * kRadix); i += kHistBlock) {
         uint32_t c = 0;
 #pragma unroll 8
         for (int k = 0; k < C; ++k) c += s_hist[i * C + k];
-        if (c) atomicAdd(&bins[i], c);
+        if (c) seen |= __hip_atomic_fetch_add(&bins[i], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // zero the look-back state of pass 0
     const uint64_t stride = (uint64_t)gridDim.x * kHistBlock;
     for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear0_words; i += stride) clear0[i] = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear1_words; i += stride) clear1[i] = 0;
+
+    // the last workgroup to arrive plans the passes (hot digits, skipped
+    // passes, buffer routing) from the finished bins
+    __shared__ uint32_t s_last, s_trivial[16];
+    if (tid == 0) s_last = 0;
+    __syncthreads();
+    if (seen == 0xFFFFFFFFu) s_last = 2;  // (a bin below 2^32 never reads so) every add's result is awaited here
+    __syncthreads();
+    if (tid == 0) s_last |= ticket(arrivals) == gridDim.x - 1 ? 1u : 0u;
+    __syncthreads();
+    if (s_last & 1u) rs_make_plan<kHistBlock>(bins, (uint32_t)P, n, hot, plan, s_trivial);
 }
 
 // ------------------------------------------------------------------ onesweep pass
@@ -654,7 +671,7 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     L.batches = ceil_div(L.tiles, kBatch);
     L.bins_off = 0;
     L.hot_off = L.passes * kRadix * 4;  // hot digits, then the pass plan: one word each per pass
-    L.tc_off = align_up(L.hot_off + 2 * L.passes * 4, 256);
+    L.tc_off = align_up(L.hot_off + (2 * L.passes + 1) * 4, 256);  // + the histogram's arrival counter
     L.tc_words = L.tiles * kRadix;
     L.bw_off = L.tc_off + align_up(2 * L.tc_words * 4, 256);
     L.bw_words = L.batches * kRadix;
@@ -692,7 +709,8 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     UV *vtmp = reinterpret_cast<UV *>(t + L.vtmp_off);
     const int P = (int)L.passes;
 
-    LCPP_LAUNCH("rs_init", s, rs_init_kernel<<<1, 256, 0, s>>>(bins, P * kRadix));
+    // bins, hot digits, plan and the histogram's arrival counter are contiguous
+    LCPP_LAUNCH("rs_init", s, rs_init_kernel<<<1, 256, 0, s>>>(bins, P * kRadix + 2 * P + 1));
     LCPP_CHECK_LAUNCH();
     {
         // one 1024-thread workgroup per CU (128 KB of LDS each)
@@ -713,11 +731,10 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         grid = ceil_div(n, chunk);
         LCPP_LAUNCH("rs_histogram", s,
                     rs_histogram_kernel<UK, KIND><<<(uint32_t)grid, kHistBlock, lds, s>>>(
-                        kin, n, chunk, bins, tc[0], L.tc_words, reinterpret_cast<uint32_t *>(bw[0]), 2 * L.bw_words, flip));
+                        kin, n, chunk, bins, tc[0], L.tc_words, reinterpret_cast<uint32_t *>(bw[0]), 2 * L.bw_words, flip,
+                        plan + P, hot, plan));
         LCPP_CHECK_LAUNCH();
     }
-    LCPP_LAUNCH("rs_hot", s, rs_hot_kernel<<<1, 256, 0, s>>>(bins, (uint32_t)P, n, hot, plan));
-    LCPP_CHECK_LAUNCH();
     // XCD run length: 8R <= half the onesweep workgroups resident at once
     static DeviceCache run_cache;  // log2(R) + 1, or -1 when the occupancy query fails
     const int lr1 = device_cached(run_cache, [] {
