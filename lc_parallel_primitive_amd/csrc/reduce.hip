@@ -29,20 +29,21 @@ namespace lcpp {
 namespace {
 
 constexpr int kRedBlock = 256;
-// Geometry (16-byte vectors per thread per tile, most workgroups), measured
-// at 2^28 int32 (us, Sum / ArgMin): 2048 x 8: 158 / 163; 1024 x 16: 154;
-// 512 x 16: 152 / 181; 512 x 32: 150 / 177; 256 x 32: 186 / 289; 512 x 48:
-// 154 / 191.  Plain folds take 512 workgroups of 32 vectors (two per CU,
-// each streaming 2 MiB); the (value, index) folds keep 2048 x 8.
+// Geometry (most workgroups x 16-byte vectors per thread per tile), measured
+// at 2^28 int32 (us, Sum / ArgMin): 2048 x 8: 158 / 163; 1024 x 16: 154 /
+// 159; 1024 x 12: - / 157; 4096 x 4: - / 162; 512 x 16: 152 / 181; 512 x
+// 32: 150 / 177; 256 x 32: 186 / 289; 512 x 48: 154 / 191.  Plain folds take
+// 512 workgroups of 32 vectors (two per CU, each streaming 2 MiB); the
+// (value, index) folds 1024 of 12.
 template <bool ARG>
 constexpr int red_vecs()
 {
-    return ARG ? 8 : 32;
+    return ARG ? 12 : 32;
 }
 template <bool ARG>
 constexpr uint32_t red_max_grid()
 {
-    return ARG ? 2048 : 512;
+    return ARG ? 1024 : 512;
 }
 
 template <class T, bool ARG>

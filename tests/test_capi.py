@@ -57,7 +57,7 @@ def _q(fn, *args):
 
 
 def test_temp_bytes_queries(L):
-    # reduce: one partial per workgroup (<= 2048), none when one workgroup suffices
+    # reduce: one partial per workgroup (<= 512; <= 1024 for arg), none when one workgroup suffices
     assert _q(L.lcpp_reduce_temp_bytes, 0, 0) == (0, 0)
     assert _q(L.lcpp_reduce_temp_bytes, 0, 8192) == (0, 0)
     rc, b = _q(L.lcpp_reduce_temp_bytes, 0, 1 << 28)  # one partial per workgroup, at most 512
@@ -68,9 +68,9 @@ def test_temp_bytes_queries(L):
     assert _q(L.lcpp_reduce_temp_bytes, 0, 32769) == (0, 256)
     # arg reduce: one (value, index) partial per workgroup
     rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 2, 1 << 28)
-    assert rc == 0 and b == 2048 * 8
+    assert rc == 0 and b == 1024 * 8
     rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 5, 1 << 28)
-    assert rc == 0 and b == 2048 * 16
+    assert rc == 0 and b == 1024 * 16
     assert _q(L.lcpp_reduce_arg_temp_bytes, 0, 100) == (0, 0)
     # scan: one packed 64-bit word per tile (two for 64-bit types), counted for
     # the smaller of the exclusive (20480 / 10240) and inclusive (16384 / 8192;

@@ -47,7 +47,7 @@ def test_kat_min_max_shuffled(gpu):
     assert run("Sum", d, a.size, np.int32) == exp[2]
 
 
-# tiles hold 32768 4-byte / 16384 8-byte elements (8192 / 4096 for Arg*); at
+# tiles hold 32768 4-byte / 16384 8-byte elements (12288 / 6144 for Arg*); at
 # 20M elements the grid is at its 512-workgroup cap with a ragged last chunk
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("n", [1, 63, 4097, 16384, 16385, 32768, 32769, 1_000_003, 20_000_003])
@@ -146,8 +146,10 @@ def test_arg_kat_shuffled(gpu):
     assert run_arg(True, d, a.size, np.int32) == (4095, int(np.nonzero(a == 4095)[0][0]))
 
 
+# Arg* tiles hold 12288 4-byte / 6144 8-byte elements; at 20M elements the
+# grid is at its 1024-workgroup cap with a ragged last chunk
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("n", [1, 63, 4097, 32768, 1_000_003])
+@pytest.mark.parametrize("n", [1, 63, 4097, 6144, 6145, 12288, 12289, 32768, 1_000_003, 20_000_003])
 def test_arg_vs_oracle_with_ties(gpu, dtype, n):
     import gpu_util as g
 
