@@ -16,7 +16,12 @@
  * Errors: the reference asserts in debug builds (lcpp_check, runtime/core.h
  * :56-67) and ignores failures in release.  Here every call returns through
  * check(): debug builds print the status and abort, release builds keep the
- * last status, readable with last_status().
+ * last status, readable with last_status().  With a debug stream
+ * (create(device, &stream)), as the reference's lcpp_check commits and
+ * synchronizes, every call is synchronized and the device status word in its
+ * temp storage is read (lcpp_temp_status), so a look-back wait that gave up
+ * (LCPP_ERR_LOOKBACK_TIMEOUT) or a failed kernel (LCPP_ERR_HIP) is reported
+ * by the call that caused it; this also holds in release builds.
  *
  * Template parameters <BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD> are accepted
  * for source compatibility; the geometry is fixed per dtype inside the
@@ -124,8 +129,11 @@ class LuisaModule {
     [[nodiscard]] int last_status() const noexcept { return m_last_status; }
 
   protected:
-    void check(int status, const char *what)
+    // `stream` / `temp` are the call's stream and temp storage; without a
+    // debug stream they are not touched.
+    void check(int status, const char *what, void *stream, BufferView<uint> temp = {})
     {
+        if (status == LCPP_OK && m_debug_stream) status = lcpp_temp_status(temp.data(), temp.size_bytes(), stream);
         m_last_status = status;
 #ifndef NDEBUG
         if (status != LCPP_OK) {
@@ -159,21 +167,21 @@ class DeviceReduce : public LuisaModule {
     {
         check(lcpp_reduce_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
                               num_item, cmdlist.stream),
-              "DeviceReduce::Sum");
+              "DeviceReduce::Sum", cmdlist.stream, temp_storage);
     }
     template <class T>
     void Min(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out, size_t num_item)
     {
         check(lcpp_reduce_min(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
                               num_item, cmdlist.stream),
-              "DeviceReduce::Min");
+              "DeviceReduce::Min", cmdlist.stream, temp_storage);
     }
     template <class T>
     void Max(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out, size_t num_item)
     {
         check(lcpp_reduce_max(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
                               num_item, cmdlist.stream),
-              "DeviceReduce::Max");
+              "DeviceReduce::Max", cmdlist.stream, temp_storage);
     }
     /* device/device_reduce.h:94-107 */
     template <class T>
@@ -190,7 +198,7 @@ class DeviceReduce : public LuisaModule {
     {
         check(lcpp_reduce_argmin(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                  d_out.data(), d_index_out.data(), num_item, cmdlist.stream),
-              "DeviceReduce::ArgMin");
+              "DeviceReduce::ArgMin", cmdlist.stream, temp_storage);
     }
     /* device/device_reduce.h:229-272 */
     template <class T>
@@ -199,7 +207,7 @@ class DeviceReduce : public LuisaModule {
     {
         check(lcpp_reduce_argmax(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                  d_out.data(), d_index_out.data(), num_item, cmdlist.stream),
-              "DeviceReduce::ArgMax");
+              "DeviceReduce::ArgMax", cmdlist.stream, temp_storage);
     }
     /* device/device_reduce.h:331-348 */
     template <class T, class ReduceOp, class TransformOp>
@@ -209,7 +217,7 @@ class DeviceReduce : public LuisaModule {
         check(lcpp_reduce_transform(dtype_of<T>(), reduce_op_of<ReduceOp>(), transform_of<TransformOp>(),
                                     temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
                                     num_item, &init, cmdlist.stream),
-              "DeviceReduce::TransformReduce");
+              "DeviceReduce::TransformReduce", cmdlist.stream, temp_storage);
     }
     /* device/device_reduce.h:110-125 */
     template <class KeyType, class ValueType>
@@ -230,7 +238,7 @@ class DeviceReduce : public LuisaModule {
                                  temp_storage.data(), temp_storage.size_bytes(), d_keys_in.data(), d_values_in.data(),
                                  d_unique_out.data(), g_aggregates_out.data(), g_num_runs_out.data(), num_elements,
                                  cmdlist.stream),
-              "DeviceReduce::ReduceByKey");
+              "DeviceReduce::ReduceByKey", cmdlist.stream, temp_storage);
     }
 };
 
@@ -252,7 +260,7 @@ class DeviceScan : public LuisaModule {
     {
         check(lcpp_scan_exclusive_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                       d_out.data(), num_items, cmdlist.stream),
-              "DeviceScan::ExclusiveSum");
+              "DeviceScan::ExclusiveSum", cmdlist.stream, temp_storage);
     }
     template <class T>
     void InclusiveSum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
@@ -260,7 +268,7 @@ class DeviceScan : public LuisaModule {
     {
         check(lcpp_scan_inclusive_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                       d_out.data(), num_items, cmdlist.stream),
-              "DeviceScan::InclusiveSum");
+              "DeviceScan::InclusiveSum", cmdlist.stream, temp_storage);
     }
     /* device/device_scan.h:91-107 */
     template <class KeyType, class ValueType>
@@ -280,7 +288,7 @@ class DeviceScan : public LuisaModule {
                                          temp_storage.data(), temp_storage.size_bytes(), d_keys_in.data(),
                                          d_values_in.data(), d_values_out.data(), num_items, &initial_value,
                                          cmdlist.stream),
-              "DeviceScan::ExclusiveScanByKey");
+              "DeviceScan::ExclusiveScanByKey", cmdlist.stream, temp_storage);
     }
     /* device/device_scan.h:256-303 (heads get scan_op(value, init); the reference gives init) */
     template <class KeyType, class ValueType, class ScanOp>
@@ -292,7 +300,7 @@ class DeviceScan : public LuisaModule {
                                          temp_storage.data(), temp_storage.size_bytes(), d_keys_in.data(),
                                          d_values_in.data(), d_values_out.data(), num_items, &initial_value,
                                          cmdlist.stream),
-              "DeviceScan::InclusiveScanByKey");
+              "DeviceScan::InclusiveScanByKey", cmdlist.stream, temp_storage);
     }
     /* device/device_scan.h:306-322 */
     template <class T>
@@ -302,7 +310,7 @@ class DeviceScan : public LuisaModule {
         check(lcpp_scan_exclusive_sum_by_key(dtype_of<T>(), dtype_of<T>(), temp_storage.data(),
                                              temp_storage.size_bytes(), d_keys_in.data(), d_values_in.data(),
                                              d_values_out.data(), num_items, cmdlist.stream),
-              "DeviceScan::ExclusiveSumByKey");
+              "DeviceScan::ExclusiveSumByKey", cmdlist.stream, temp_storage);
     }
     /* device/device_scan.h:324-339 */
     template <class T>
@@ -312,7 +320,7 @@ class DeviceScan : public LuisaModule {
         check(lcpp_scan_inclusive_sum_by_key(dtype_of<T>(), dtype_of<T>(), temp_storage.data(),
                                              temp_storage.size_bytes(), d_keys_in.data(), d_values_in.data(),
                                              d_values_out.data(), num_items, cmdlist.stream),
-              "DeviceScan::InclusiveSumByKey");
+              "DeviceScan::InclusiveSumByKey", cmdlist.stream, temp_storage);
     }
 };
 
@@ -343,7 +351,7 @@ class DeviceRadixSort : public LuisaModule {
         check(lcpp_radix_sort_pairs(dtype_of<KeyType>(), dtype_of<ValueType>(), temp_storage.data(),
                                     temp_storage.size_bytes(), d_keys_in.data(), d_keys_out.data(),
                                     d_values_in.data(), d_values_out.data(), num_items, cmdlist.stream),
-              "DeviceRadixSort::SortPairs");
+              "DeviceRadixSort::SortPairs", cmdlist.stream, temp_storage);
     }
     template <class KeyType>
     void SortKeys(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
@@ -351,7 +359,7 @@ class DeviceRadixSort : public LuisaModule {
     {
         check(lcpp_radix_sort_keys(dtype_of<KeyType>(), temp_storage.data(), temp_storage.size_bytes(),
                                    d_keys_in.data(), d_keys_out.data(), num_items, cmdlist.stream),
-              "DeviceRadixSort::SortKeys");
+              "DeviceRadixSort::SortKeys", cmdlist.stream, temp_storage);
     }
     /* device/device_radix_sort.h:156-170 */
     template <class KeyType, class ValueType>
@@ -362,7 +370,7 @@ class DeviceRadixSort : public LuisaModule {
         check(lcpp_radix_sort_pairs_descending(dtype_of<KeyType>(), dtype_of<ValueType>(), temp_storage.data(),
                                                temp_storage.size_bytes(), d_keys_in.data(), d_keys_out.data(),
                                                d_values_in.data(), d_values_out.data(), num_items, cmdlist.stream),
-              "DeviceRadixSort::SortPairsDescending");
+              "DeviceRadixSort::SortPairsDescending", cmdlist.stream, temp_storage);
     }
     /* device/device_radix_sort.h:172-184 */
     template <class KeyType>
@@ -371,7 +379,7 @@ class DeviceRadixSort : public LuisaModule {
     {
         check(lcpp_radix_sort_keys_descending(dtype_of<KeyType>(), temp_storage.data(), temp_storage.size_bytes(),
                                               d_keys_in.data(), d_keys_out.data(), num_items, cmdlist.stream),
-              "DeviceRadixSort::SortKeysDescending");
+              "DeviceRadixSort::SortKeysDescending", cmdlist.stream, temp_storage);
     }
 };
 
@@ -405,7 +413,7 @@ class DeviceSegmentReduce : public LuisaModule {
         check(lcpp_segment_reduce(dtype_of<T>(), reduce_op_of<ReduceOp>(), temp_storage.data(),
                                   temp_storage.size_bytes(), d_in.data(), d_out.data(), num_segments,
                                   d_begin_offsets.data(), d_end_offsets.data(), &initial_value, cmdlist.stream),
-              "DeviceSegmentReduce::Reduce");
+              "DeviceSegmentReduce::Reduce", cmdlist.stream);
     }
     /* device/device_segment_reduce.h:109-123 */
     template <class T, class ReduceOp>
@@ -415,7 +423,7 @@ class DeviceSegmentReduce : public LuisaModule {
         check(lcpp_segment_reduce_fixed(dtype_of<T>(), reduce_op_of<ReduceOp>(), temp_storage.data(),
                                         temp_storage.size_bytes(), d_in.data(), d_out.data(), num_segments,
                                         segment_size, &initial_value, cmdlist.stream),
-              "DeviceSegmentReduce::Reduce");
+              "DeviceSegmentReduce::Reduce", cmdlist.stream);
     }
     template <class T>
     void Sum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
@@ -424,7 +432,7 @@ class DeviceSegmentReduce : public LuisaModule {
         check(lcpp_segment_reduce_sum(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                       d_out.data(), num_segments, d_begin_offsets.data(), d_end_offsets.data(),
                                       cmdlist.stream),
-              "DeviceSegmentReduce::Sum");
+              "DeviceSegmentReduce::Sum", cmdlist.stream);
     }
     template <class T>
     void Sum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
@@ -468,7 +476,7 @@ class DeviceSegmentReduce : public LuisaModule {
         check(lcpp_segment_reduce_argmax(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                          d_out.data(), d_index_out.data(), num_segments, d_begin_offsets.data(),
                                          d_end_offsets.data(), cmdlist.stream),
-              "DeviceSegmentReduce::ArgMax");
+              "DeviceSegmentReduce::ArgMax", cmdlist.stream);
     }
     /* device/device_segment_reduce.h:236-272 */
     template <class T>
@@ -478,7 +486,7 @@ class DeviceSegmentReduce : public LuisaModule {
         check(lcpp_segment_reduce_argmax_fixed(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(),
                                                d_in.data(), d_out.data(), d_index_out.data(), num_segments,
                                                segment_size, cmdlist.stream),
-              "DeviceSegmentReduce::ArgMax");
+              "DeviceSegmentReduce::ArgMax", cmdlist.stream);
     }
     /* device/device_segment_reduce.h:274-312 (the reference spells this overload Argmin) */
     template <class T>
@@ -489,7 +497,7 @@ class DeviceSegmentReduce : public LuisaModule {
         check(lcpp_segment_reduce_argmin(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(), d_in.data(),
                                          d_out.data(), d_index_out.data(), num_segments, d_begin_offsets.data(),
                                          d_end_offsets.data(), cmdlist.stream),
-              "DeviceSegmentReduce::ArgMin");
+              "DeviceSegmentReduce::ArgMin", cmdlist.stream);
     }
     template <class T>
     void Argmin(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
@@ -506,7 +514,7 @@ class DeviceSegmentReduce : public LuisaModule {
         check(lcpp_segment_reduce_argmin_fixed(dtype_of<T>(), temp_storage.data(), temp_storage.size_bytes(),
                                                d_in.data(), d_out.data(), d_index_out.data(), num_segments,
                                                segment_size, cmdlist.stream),
-              "DeviceSegmentReduce::ArgMin");
+              "DeviceSegmentReduce::ArgMin", cmdlist.stream);
     }
 };
 

@@ -12,7 +12,8 @@
  *     nothing is thrown across the ABI.
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *     All work is enqueued asynchronously on it; results are valid once the
- *     stream is synchronized.  No call synchronizes the stream.
+ *     stream is synchronized.  No primitive synchronizes the stream (only the
+ *     validation calls lcpp_temp_status and lcpp_stream_sync do).
  *   - The caller owns all memory, including temp storage sized by the
  *     matching *_temp_bytes query.  The library never allocates device
  *     memory on these paths.  Temp storage must be 256-byte aligned.
@@ -64,13 +65,46 @@ typedef enum lcpp_status {
     LCPP_ERR_INVALID_ARG = -1,      /* null pointer, misaligned temp, size out of range */
     LCPP_ERR_TEMP_TOO_SMALL = -2,   /* temp_bytes < the *_temp_bytes query result */
     LCPP_ERR_UNSUPPORTED_DTYPE = -3,
-    LCPP_ERR_HIP = -4               /* a HIP runtime call or kernel launch failed */
+    LCPP_ERR_HIP = -4,              /* a HIP runtime call or kernel launch failed */
+    LCPP_ERR_LOOKBACK_TIMEOUT = -5  /* reported by lcpp_temp_status: a look-back wait gave up,
+                                       so that call's output is wrong */
 } lcpp_status;
+
+/* Bits of the device status word kept in the first 4 bytes of temp storage. */
+#define LCPP_DEVICE_STATUS_LOOKBACK_TIMEOUT 1u
 
 /* Library version (LCPP_AMD_VERSION of the build). */
 int lcpp_version(void);
 /* Static, human-readable name of a status code. */
 const char *lcpp_status_string(int status);
+
+/* ---------------------------------------------------------------------
+ * Device-side status (the counterpart of the reference's debug-stream check,
+ * lcpp_check in runtime/core.h:56-64, which commits, synchronizes and asserts
+ * after each step).  Every primitive that uses temp storage reserves its
+ * first 256 bytes as a status header; the call's first kernel zeroes the
+ * status word and a decoupled look-back wait that exhausts its bounded spin
+ * sets LCPP_DEVICE_STATUS_LOOKBACK_TIMEOUT in it (its output is then wrong;
+ * the kernels still finish).  A wait can only give up when the workgroups it
+ * waits on cannot run, e.g. when other kernels hold the whole device.
+ * ------------------------------------------------------------------- */
+/* Synchronizes `stream`, then reads the status word of the last call that used
+ * `temp` (temp_bytes as passed to that call; calls whose temp query is 0 do not
+ * use temp storage).  Returns LCPP_OK, LCPP_ERR_LOOKBACK_TIMEOUT or LCPP_ERR_HIP.
+ * temp == NULL or temp_bytes < 256: synchronizes and returns LCPP_OK.  This is
+ * the one function here that synchronizes (a debug / validation path). */
+int lcpp_temp_status(const void *temp, size_t temp_bytes, void *stream);
+/* The lcpp_status a device status word stands for (pure host arithmetic). */
+int lcpp_device_status_decode(uint32_t word);
+/* hipStreamSynchronize(stream): LCPP_OK or LCPP_ERR_HIP. */
+int lcpp_stream_sync(void *stream);
+/* Test hook, process-wide: look-back waits give up after `spin_limit` re-polls
+ * (0 = the default, about half a second of polling), and the tile or sort tile
+ * numbered `withhold_tile` does not publish its look-back words
+ * (0xFFFFFFFF = none), so the waits behind it give up and report through the
+ * status word.  Outputs of calls made while a tile is withheld are wrong.  Not
+ * for production use; calls running concurrently see the same setting. */
+int lcpp_test_set_lookback_fault(uint32_t withhold_tile, uint32_t spin_limit);
 
 /* ---------------------------------------------------------------------
  * DeviceReduce — device/device_reduce.h

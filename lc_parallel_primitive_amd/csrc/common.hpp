@@ -324,12 +324,39 @@ __device__ __forceinline__ void buf_st_elem(__amdgpu_buffer_rsrc_t r, uint32_t v
     }
 }
 
-// ---------------------------------------------------------------- misc
-// Upper bound on the polls of one look-back wait (~1 s of s_sleep-paced
+// ---------------------------------------------------------------- waits and the status word
+// Upper bound on the polls of one look-back wait (~0.5 s of s_sleep-paced
 // polling).  A wait that exceeds it gives up, so a kernel always drains even
-// if a predecessor's word were never published (the result is then wrong,
-// which the parity tests report, instead of a hung GPU).
+// if a predecessor's word were never published; the give-up is recorded in
+// the call's status word (below), so the result is reported as wrong instead
+// of a hung GPU.
 constexpr uint32_t kSpinLimit = 1u << 20;
+
+// Every primitive that uses temp storage keeps a status header in its first
+// 256 bytes; the first 32-bit word is zeroed by the call's first kernel and
+// collects LCPP_DEVICE_STATUS_* bits (lcpp_amd.h), read back by
+// lcpp_temp_status().  The rest of the temp layout starts after the header.
+constexpr uint64_t kStatusBytes = 256;
+
+// What a kernel that waits on other workgroups needs besides its data:
+// where a wait that gives up reports, how long a wait lasts, and a test hook
+// (a tile that never publishes, so the waits behind it give up on purpose:
+// the kernels still drain normally, every access stays in bounds).
+struct WaitCtl {
+    uint32_t *status;     // status word (zeroed earlier in the same call)
+    uint32_t spin_limit;  // re-polls before a wait gives up (>= 1)
+    uint32_t withhold;    // tile that does not publish its look-back words (~0u: none)
+};
+__device__ __forceinline__ void report_timeout(const WaitCtl &c)
+{
+    __hip_atomic_fetch_or(c.status, (uint32_t)LCPP_DEVICE_STATUS_LOOKBACK_TIMEOUT, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+}
+// Host: the WaitCtl of a call whose status word is `status` (the test hooks
+// set by lcpp_test_set_lookback_fault apply).
+WaitCtl wait_ctl(uint32_t *status);
+
+// ---------------------------------------------------------------- misc
 
 __host__ __device__ constexpr uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr uint64_t align_up(uint64_t a, uint64_t b) { return ceil_div(a, b) * b; }

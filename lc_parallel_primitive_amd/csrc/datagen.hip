@@ -90,9 +90,128 @@ __global__ __launch_bounds__(256) void copy_probe_kernel(const u32x4c *__restric
     if (b + 256 < nvec) __builtin_nontemporal_store(v1, out + b + 256);
 }
 
+// ---------------------------------------------------------------- test checkers
+// Device restatements of the oracle's O(N) property checkers, for sort sizes
+// whose host check would take minutes.  The GPU tests pin them against the
+// host checkers (and planted mistakes) at small sizes.
+//
+// Sortedness and multiset hashes of a u32 array: out[0] += number of i with
+// a[i] > a[i+1]; out[1] += sum of a[i]; out[2] += sum of mix64(a[i]) (both
+// sums mod 2^64 are order-independent, so equal multisets give equal sums).
+__global__ __launch_bounds__(256) void sorted_hash_kernel(const uint32_t *__restrict__ a, uint64_t n,
+                                                          unsigned long long *out)
+{
+    uint64_t desc = 0, s1 = 0, s2 = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+        const uint32_t x = a[i];
+        if (i + 1 < n && x > a[i + 1]) ++desc;
+        s1 += x;
+        s2 += mix64(x);
+    }
+    atomicAdd(&out[0], (unsigned long long)desc);
+    atomicAdd(&out[1], (unsigned long long)s1);
+    atomicAdd(&out[2], (unsigned long long)s2);
+}
+
+// Stable-pairs checker (values = input index): counts positions i where
+// vals_out[i] >= n, keys_out[i] != keys_in[vals_out[i]], or (keys_out[i],
+// vals_out[i]) is not strictly below (keys_out[i+1], vals_out[i+1]).  Zero
+// bad positions <=> the output is the stable sort of the input: the pairs
+// are distinct, so the n values < n form a permutation.
+__global__ __launch_bounds__(256) void stable_pairs_kernel(const uint32_t *__restrict__ kin,
+                                                           const uint32_t *__restrict__ kout,
+                                                           const uint32_t *__restrict__ vout, uint64_t n,
+                                                           unsigned long long *bad)
+{
+    uint64_t b = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+        const uint32_t v = vout[i], k = kout[i];
+        if (v >= n || kin[v] != k) ++b;
+        if (i + 1 < n) {
+            const uint32_t k1 = kout[i + 1], v1 = vout[i + 1];
+            if (k > k1 || (k == k1 && v >= v1)) ++b;
+        }
+    }
+    atomicAdd(bad, (unsigned long long)b);
+}
+
+// Probe of the LDS ordering the sort's stable ranking relies on: in one
+// returning LDS atomic add instruction, lanes that hit the same address get
+// their old values in lane order.  Each wave repeatedly draws a digit per
+// lane (pattern 0: uniform over 256; 1: digit 0 with probability 1/3, else
+// uniform; 2: one digit for the whole wave; 3: two digits), adds 1 at its
+// digit's counter and checks that every lane's result equals the counter's
+// value before the instruction plus the number of lower lanes with the same
+// digit.  Every LDS index is < 256 + 64 per wave; violations are counted.
+__global__ __launch_bounds__(256) void lds_order_probe_kernel(uint64_t seed, uint32_t pattern, uint32_t rounds,
+                                                              unsigned long long *violations)
+{
+    __shared__ uint32_t cnt[4][256];
+    __shared__ uint32_t before[4][256];
+    const uint32_t lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const uint32_t w = threadIdx.x / 64;
+    for (uint32_t i = lane; i < 256; i += 64) cnt[w][i] = 0;
+    __builtin_amdgcn_wave_barrier();
+    uint64_t bad = 0;
+    const uint64_t gid = (uint64_t)blockIdx.x * 4 + w;
+    for (uint32_t r = 0; r < rounds; ++r) {
+        const uint64_t h = word(seed, (gid * rounds + r) * 64 + lane);
+        uint32_t d;
+        if (pattern == 0) d = (uint32_t)h & 255u;
+        else if (pattern == 1) d = ((h >> 32) % 3 == 0) ? 0u : ((uint32_t)h & 255u);
+        else if (pattern == 2) d = (uint32_t)word(seed, gid * rounds + r) & 255u;
+        else d = ((uint32_t)h & 1u) ? 17u : 200u;
+        // counter values before this instruction
+        for (uint32_t i = lane; i < 256; i += 64) before[w][i] = cnt[w][i];
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t got = atomicAdd(&cnt[w][d], 1u);
+        // lower lanes with the same digit, from one ballot per candidate
+        uint32_t lower = 0;
+        for (uint32_t j = 0; j < 64; ++j) {
+            const uint32_t dj = (uint32_t)__builtin_amdgcn_readlane((int)d, (int)j);
+            lower += (j < lane && dj == d) ? 1u : 0u;
+        }
+        if (got != before[w][d] + lower) ++bad;
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (bad) atomicAdd(violations, (unsigned long long)bad);
+}
+
 }  // namespace
 
 extern "C" {
+
+// out[3] (device, zeroed by the caller): descents, sum, sum of mix64.
+int lcpp_dg_sorted_hash_u32(const void *a, uint64_t n, void *out, void *stream)
+{
+    if (!out || (n && !a)) return -1;
+    sorted_hash_kernel<<<2048, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint32_t *>(a), n, static_cast<unsigned long long *>(out));
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+// *bad (device, zeroed by the caller) += bad positions of a stable u32/u32
+// sort whose values were the input indices.
+int lcpp_dg_check_stable_pairs_u32(const void *keys_in, const void *keys_out, const void *vals_out, uint64_t n,
+                                   void *bad, void *stream)
+{
+    if (!bad || (n && (!keys_in || !keys_out || !vals_out))) return -1;
+    stable_pairs_kernel<<<2048, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint32_t *>(keys_in), static_cast<const uint32_t *>(keys_out),
+        static_cast<const uint32_t *>(vals_out), n, static_cast<unsigned long long *>(bad));
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+// *violations (device, zeroed by the caller) += lanes whose atomic result
+// broke lane order, over `waves` waves x `rounds` instructions.
+int lcpp_dg_lds_order_probe(uint64_t seed, uint32_t pattern, uint32_t waves, uint32_t rounds, void *violations,
+                            void *stream)
+{
+    if (!violations || pattern > 3 || waves == 0 || (waves & 3)) return -1;
+    lds_order_probe_kernel<<<waves / 4, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        seed, pattern, rounds, static_cast<unsigned long long *>(violations));
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
 
 // n must be a multiple of 4 and both pointers 16-byte aligned.
 int lcpp_copy_probe_u32(const void *in, void *out, uint64_t n, void *stream)

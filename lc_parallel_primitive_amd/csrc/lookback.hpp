@@ -16,7 +16,9 @@
 //
 // The prefix wait is executed by one wave: lane l < 16 polls predecessor
 // top - l, all loads issued before any wait, and the wave stops at the
-// nearest INCLUSIVE tile, waiting only for closer predecessors.
+// nearest INCLUSIVE tile, waiting only for closer predecessors.  A wait
+// that exhausts its bounded spin gives up and records the fact in the call's
+// status word (WaitCtl), so a wrong result is reported, never a hung GPU.
 #pragma once
 
 #include "common.hpp"
@@ -45,8 +47,9 @@ __device__ __forceinline__ T lb_from_bits(uint64_t b)
 }
 
 template <class T>
-__device__ __forceinline__ void lb_publish(uint64_t *words, uint32_t tile, T v, uint32_t status)
+__device__ __forceinline__ void lb_publish(uint64_t *words, uint32_t tile, T v, uint32_t status, const WaitCtl &ctl)
 {
+    if (tile == ctl.withhold) return;  // test hook: this tile never publishes
     const uint64_t b = lb_bits(v);
     if constexpr (sizeof(T) == 4) {
         st_relaxed(&words[tile], (b << 32) | status);
@@ -69,7 +72,7 @@ constexpr int kLbPollWidth = 16;
 // predecessor's inclusive value.  Every lane returns it.  `op` must be
 // commutative (sum, min, max): a window is reduced as a tree.
 template <class T, class Op>
-__device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T identity)
+__device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T identity, const WaitCtl &ctl)
 {
     const uint32_t lane = lane_id();
     T excl = identity;
@@ -106,9 +109,12 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
         const uint64_t incl = ballot(s == kStInclusive);
         const uint32_t stop = incl ? (uint32_t)__builtin_ctzll(incl) : (uint32_t)(kWave - 1);
         const bool in_range = lane <= stop;
-        if (ballot(in_range && s == kStInvalid) != 0 && ++spins < kSpinLimit) {
-            __builtin_amdgcn_s_sleep(1);
-            continue;  // re-poll the same window
+        if (ballot(in_range && s == kStInvalid) != 0) {
+            if (++spins < ctl.spin_limit) {
+                __builtin_amdgcn_s_sleep(1);
+                continue;  // re-poll the same window
+            }
+            if (lane == 0) report_timeout(ctl);  // give up with what has been published
         }
         const T acc = in_range ? v : identity;
         const bool found = incl != 0;
@@ -123,16 +129,17 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
 // INCLUSIVE(prefix op agg).  Returns the exclusive prefix (identity for
 // tile 0) in every lane.
 template <class T, class Op>
-__device__ __forceinline__ T lb_scan_tile(uint64_t *words, uint32_t tile, T agg, Op op, T identity)
+__device__ __forceinline__ T lb_scan_tile(uint64_t *words, uint32_t tile, T agg, Op op, T identity,
+                                          const WaitCtl &ctl)
 {
     const uint32_t lane = lane_id();
     if (tile == 0) {
-        if (lane == 0) lb_publish(words, 0, agg, kStInclusive);
+        if (lane == 0) lb_publish(words, 0, agg, kStInclusive, ctl);
         return identity;
     }
-    if (lane == 0) lb_publish(words, tile, agg, kStPartial);
-    const T excl = lb_wait_prefix(words, tile, op, identity);
-    if (lane == 0) lb_publish(words, tile, op(excl, agg), kStInclusive);
+    if (lane == 0) lb_publish(words, tile, agg, kStPartial, ctl);
+    const T excl = lb_wait_prefix(words, tile, op, identity, ctl);
+    if (lane == 0) lb_publish(words, tile, op(excl, agg), kStInclusive, ctl);
     return excl;
 }
 
@@ -142,12 +149,12 @@ __device__ __forceinline__ T lb_scan_tile(uint64_t *words, uint32_t tile, T agg,
 // a head (`need_prefix`).  A tile without a head is a plain scan tile.
 template <class T, class Op>
 __device__ __forceinline__ T lb_segmented_tile(uint64_t *words, uint32_t tile, T agg, bool has_head,
-                                              bool need_prefix, Op op, T identity)
+                                              bool need_prefix, Op op, T identity, const WaitCtl &ctl)
 {
-    if (!has_head) return lb_scan_tile(words, tile, agg, op, identity);
-    if (lane_id() == 0) lb_publish(words, tile, agg, kStInclusive);
+    if (!has_head) return lb_scan_tile(words, tile, agg, op, identity, ctl);
+    if (lane_id() == 0) lb_publish(words, tile, agg, kStInclusive, ctl);
     if (tile == 0 || !need_prefix) return identity;
-    return lb_wait_prefix(words, tile, op, identity);
+    return lb_wait_prefix(words, tile, op, identity, ctl);
 }
 
 namespace {
@@ -157,8 +164,9 @@ __global__ __launch_bounds__(256) void lb_init_kernel(uint64_t *words, uint64_t 
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) words[i] = 0;
 }
 
-// Zero `count` look-back words on stream s (grid-stride fill kernel; a
-// kernel rather than hipMemsetAsync so the call can be graph-captured).
+// Zero `count` words on stream s (grid-stride fill kernel; a kernel rather
+// than hipMemsetAsync so the call can be graph-captured).  Callers pass the
+// status header and the look-back words behind it as one range.
 int lb_init(uint64_t *words, uint64_t count, hipStream_t s, const char *name)
 {
     if (!count) return LCPP_OK;

@@ -15,15 +15,17 @@
 // the pass needs, each tile would walk ~100 predecessors per digit.  The pass
 // here is built around that:
 //
-//  * launch 0 "rs_init": zero the P digit histograms and an arrival counter.
+//  * launch 0 "rs_init": zero the status word, the P digit histograms and an
+//    arrival counter.
 //  * launch 1 "rs_histogram": one 1024-thread workgroup per CU streams a
 //    contiguous chunk of keys and counts all P = sizeof(K) 8-bit digits at
 //    once into an LDS table with 32 (16 for 8-byte keys) lane-private copies
 //    of every counter, so that equal digits in one wave (skewed or constant
 //    key bytes) never hit one LDS address; flushed with one global atomic per
 //    non-zero bin.  It also zeroes the look-back state of pass 0.  The last
-//    workgroup to finish (the arrival counter) finds each pass's hot digit
-//    and plans the passes from the finished histograms (below).
+//    workgroup to finish (the arrival counter, release/acquire at agent
+//    scope) finds each pass's hot digit and plans the passes from the
+//    finished histograms (below).
 //  * launches 2..P+1 "rs_onesweep": one 16384-key tile (8192 for 8-byte keys
 //    or values) per 512-thread workgroup.  No ticket: tiles are mapped from
 //    the workgroup id so that every R consecutive tiles (R = 16 on a full
@@ -33,15 +35,16 @@
 //    at 2^28).  A tile only ever waits on tiles dispatched at most 8R-1
 //    workgroups after it, so R is chosen on the host such that 8R is at most
 //    half of the workgroups the device holds at once (R = 1 is plain
-//    dispatch order and always safe).
+//    dispatch order).
 //  * Ranking: keys are loaded wave-striped (lane l of wave w, item u -> key
 //    w*64*IPT + u*64 + l) so items in order u and lanes in order l are input
 //    order; a key's rank in its (wave, digit) is one returning LDS atomic add
 //    on the wave's counter for that digit.  gfx950 serves same-address LDS
-//    atomics of one instruction in lane order, so the ranks are stable (an
-//    in-bounds probe found no exception in 5e8 lane-operations over uniform,
-//    skewed and constant digits; the parity tests check stability on every
-//    run).  Ranks are kept two per register (16 bits each).
+//    atomics of one instruction in lane order, so the ranks are stable.  This
+//    is a property of the hardware, not of the ISA documentation: the GPU
+//    test suite checks it directly (a probe kernel over uniform, skewed and
+//    constant digits) and checks stability on every sort it runs.  Ranks are
+//    kept two per register (16 bits each).
 //  * Two-level decoupled look-back.  Tiles form batches of 8.  Each tile
 //    publishes its 256 digit counts once.  A tile's exclusive prefix = the
 //    exclusive prefix of its batch + the counts of the earlier tiles of its
@@ -49,9 +52,11 @@
 //    are 32-bit words {PARTIAL:1 | value}.  Batch words are 64-bit: every tile
 //    of the batch adds its counts into the low half atomically, and the
 //    batch's last tile, once it has walked the earlier batch words (waves
-//    0..3, two of them per poll), adds GLOBAL | the batch's inclusive prefix
-//    into the high half.  Every wait is on an earlier tile, and every re-poll
-//    reloads all the words it still waits on.  Words are accessed with
+//    0..3, two of them per poll), adds GLOBAL (low half, bit 31) and the
+//    batch's 32-bit inclusive prefix (high half) in one atomic, so n may use
+//    all 32 bits.  Every wait is on an earlier tile, every re-poll reloads all
+//    the words it still waits on, and a wait that exhausts its bounded spin
+//    records the give-up in the call's status word.  Words are accessed with
 //    agent-scope atomics (the 8 XCD L2s are not coherent).  Two look-back
 //    regions alternate between passes and tiles clear their slots of the
 //    other region for the next pass (no per-pass memset launch).
@@ -62,8 +67,9 @@
 //  * The pass plan is made on the device: a pass whose digit is the same for
 //    every key (from the histogram) is skipped, and the others ping-pong so
 //    that the last one writes the output.
-//  * Descending order sorts the bit-inverted sort keys (one XOR in, one out),
-//    as RadixSortTwiddle<true> does; equal keys keep their input order.
+//  * Descending order sorts the bit-inverted sort keys (one XOR in, one out,
+//    compiled only into the descending kernels), as RadixSortTwiddle<true>
+//    does; equal keys keep their input order.
 //  * Keys-only sorts reserve no value scratch (the reference reserves N
 //    values it never uses, device_radix_sort.h:118-122).
 #include "common.hpp"
@@ -80,7 +86,7 @@ constexpr int kHistBlock = 1024;
 constexpr uint32_t kLbGlobal = 0x80000000u;
 constexpr uint32_t kLbPartial = 0x40000000u;
 constexpr uint32_t kLbMask = 0x3FFFFFFFu;
-constexpr uint64_t kMaxItems = (1ull << 30) - 1;
+constexpr uint64_t kMaxItems = 0xFFFFFFFFull;  // 32-bit positions and counts
 
 enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
 
@@ -101,19 +107,31 @@ __device__ __forceinline__ UK tw_out(UK k)
     else if constexpr (KIND == kFloat) return (k & high) ? UK(k ^ high) : UK(~k);
     else return k;
 }
-// Digit of a sort key.  Sort keys are twiddled keys XOR `flip` (0 for
-// ascending, all ones for descending: RadixSortTwiddle::In,
-// agent/radix_rank_sort_operations.h:124-155).  -0.0 and +0.0 are given the
-// same digits (radix_rank_sort_operations.h:33-62, ProcessFloatMinusZero);
-// their two sort keys are adjacent, so folding either onto the other yields
-// the same stable order.
-template <class UK, int KIND>
-__device__ __forceinline__ uint32_t digit_of(UK tk, uint32_t shift, UK flip)
+// Sort key of a raw key: twiddled, then bit-inverted for descending order
+// (RadixSortTwiddle::In, agent/radix_rank_sort_operations.h:124-155).
+template <class UK, int KIND, bool DESC>
+__device__ __forceinline__ UK sort_key(UK raw)
+{
+    const UK t = tw_in<UK, KIND>(raw);
+    return DESC ? UK(~t) : t;
+}
+template <class UK, int KIND, bool DESC>
+__device__ __forceinline__ UK raw_key(UK sk)
+{
+    return tw_out<UK, KIND>(DESC ? UK(~sk) : sk);
+}
+// Digit of a sort key.  -0.0 and +0.0 are given the same digits
+// (radix_rank_sort_operations.h:33-62, ProcessFloatMinusZero); their two sort
+// keys are adjacent, so folding either onto the other yields the same stable
+// order.
+template <class UK, int KIND, bool DESC>
+__device__ __forceinline__ uint32_t digit_of(UK tk, uint32_t shift)
 {
     if constexpr (KIND == kFloat) {
         constexpr UK high = UK(1) << (sizeof(UK) * 8 - 1);
-        const UK minus_zero = UK(~high) ^ flip;  // tw_in(-0.0) ^ flip
-        if (tk == minus_zero) tk = high ^ flip;  // tw_in(+0.0) ^ flip
+        constexpr UK flip = DESC ? UK(~UK(0)) : UK(0);
+        constexpr UK minus_zero = UK(~high) ^ flip;  // sort key of -0.0
+        if (tk == minus_zero) tk = high ^ flip;      // sort key of +0.0
     }
     return (uint32_t)(tk >> shift) & (kRadix - 1);
 }
@@ -134,8 +152,8 @@ __device__ __forceinline__ uint32_t digit_excl_scan(uint32_t x, uint32_t *s_wsum
     return pre + inc - x;
 }
 
-// Look-back polls are bounded (kSpinLimit re-polls: a wait that never ends
-// would mean a broken invariant; it then gives up with what it has).
+// Look-back polls are bounded (WaitCtl::spin_limit re-polls; a wait that
+// gives up records it in the status word and continues with what it has).
 // Agent-scope polls compete with the data stream under full HBM load, so the
 // re-poll interval is long: s_sleep 16 (~1000 cycles) between polls measured
 // 2.17 ms per 2^28 u32 sort against 2.21 ms with s_sleep 1 (s_sleep 64:
@@ -158,11 +176,12 @@ __device__ __forceinline__ uint64_t ld_agent64(__amdgpu_buffer_rsrc_t r, uint32_
 // their summed digit counts: every tile of the batch adds its counts with a
 // relaxed agent-scope atomic as it publishes them, so the batch aggregate is
 // complete one publish latency after the batch's last count, with no
-// read-and-republish round trip by one of its tiles.  The high half is
-// GLOBAL | inclusive prefix through the batch, added once by the batch's last
-// tile.  Measured at 2^28 u32 keys against 32-bit {GLOBAL | PARTIAL | value}
-// words stored by the batch's last tile: 2.13 -> 2.05 ms per sort (AND-of-3
-// keys 2.15 -> 2.03 ms); SortPairs u64 -> u32 at 2^27: 5.42 -> 5.19 ms.
+// read-and-republish round trip by one of its tiles.  The batch's last tile
+// adds, in one atomic, GLOBAL into bit 31 of the low half and the batch's
+// inclusive prefix into the high half (a full 32-bit count).  Measured at
+// 2^28 u32 keys against 32-bit {GLOBAL | PARTIAL | value} words stored by
+// the batch's last tile: 2.13 -> 2.05 ms per sort (AND-of-3 keys 2.15 ->
+// 2.03 ms); SortPairs u64 -> u32 at 2^27: 5.42 -> 5.19 ms.
 constexpr uint64_t kBwArrive = 1ull << 24;
 constexpr uint32_t kBwSumMask = (1u << 24) - 1;
 // 0 = not complete yet (v = 0: the word may hold the counts of some of its
@@ -170,15 +189,15 @@ constexpr uint32_t kBwSumMask = (1u << 24) - 1;
 __device__ __forceinline__ int batch_word_state(uint64_t w, uint32_t &v)
 {
     const uint32_t hi = (uint32_t)(w >> 32), lo = (uint32_t)w;
-    const int st = (hi & kLbGlobal) ? 2 : (lo >> 24) == (uint32_t)kBatch ? 1 : 0;
-    v = st == 2 ? hi & kLbMask : st == 1 ? lo & kBwSumMask : 0u;
+    const int st = (lo & kLbGlobal) ? 2 : ((lo >> 24) & 0x7Fu) == (uint32_t)kBatch ? 1 : 0;
+    v = st == 2 ? hi : st == 1 ? lo & kBwSumMask : 0u;
     return st;
 }
 
 // ------------------------------------------------------------------ init
-__global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *bins, uint32_t nbins)
+__global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *words, uint32_t count)
 {
-    for (uint32_t i = threadIdx.x; i < nbins; i += 256) bins[i] = 0;
+    for (uint32_t i = threadIdx.x; i < count; i += 256) words[i] = 0;
 }
 
 // ------------------------------------------------------------------ hot digits, pass plan
@@ -197,8 +216,8 @@ __global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *bins, uint32_t n
 constexpr uint32_t kPlanSkip = 1u, kPlanCopy = 2u;
 constexpr int kPlanSrcShift = 2, kPlanDstShift = 4, kPlanRegionShift = 6;
 enum PlanBuf : uint32_t { kBufIn = 0, kBufTmp = 1, kBufOut = 2 };
-// Runs in the histogram's last workgroup (NT threads): the bins are read
-// with agent-scope loads, after every workgroup's adds have been counted.
+// Runs in the histogram's last workgroup (NT threads), after the acquire that
+// pairs with every workgroup's release of its bin adds.
 template <int NT>
 __device__ void rs_make_plan(const uint32_t *bins, uint32_t passes, uint64_t n, uint32_t *__restrict__ hot,
                              uint32_t *__restrict__ plan, uint32_t *s_trivial)
@@ -247,33 +266,46 @@ constexpr int hist_copies()
 {
     return sizeof(UK) == 4 ? 32 : 16;  // 128 KB of LDS either way
 }
+// Dynamic LDS: the counter table [P][256][C], then 17 words of planning state
+// for the last workgroup (the kernel has no static LDS).
+template <class UK>
+constexpr size_t hist_table_words()
+{
+    return sizeof(UK) * kRadix * hist_copies<UK>();
+}
 template <class UK>
 constexpr size_t hist_lds_bytes()
 {
-    return sizeof(UK) * kRadix * hist_copies<UK>() * 4;
+    return (hist_table_words<UK>() + 17) * 4;
 }
 
-template <class UK, int KIND>
+template <class UK, int KIND, bool DESC>
 __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     const UK *__restrict__ keys, uint64_t n, uint64_t chunk, uint32_t *bins, uint32_t *__restrict__ clear0,
-    uint64_t clear0_words, uint32_t *__restrict__ clear1, uint64_t clear1_words, UK flip, uint32_t *arrivals,
+    uint64_t clear0_words, uint32_t *__restrict__ clear1, uint64_t clear1_words, uint32_t *arrivals,
     uint32_t *__restrict__ hot, uint32_t *__restrict__ plan)
 {
     constexpr int P = sizeof(UK);
     constexpr int C = hist_copies<UK>();
-    extern __shared__ uint32_t s_hist[];  // [P][256][C]
+    extern __shared__ uint32_t s_hist[];  // [P][256][C], then s_last, s_trivial[16]
     const uint32_t tid = threadIdx.x;
     const uint32_t copy = lane_id() % C;
+    uint32_t *s_last = s_hist + hist_table_words<UK>(), *s_trivial = s_last + 1;
     for (uint32_t i = tid; i < (uint32_t)(P * kRadix * C); i += kHistBlock) s_hist[i] = 0;
+    // zero the look-back state of pass 0 (before the counts, so that the
+    // release below covers these stores as well)
+    const uint64_t stride = (uint64_t)gridDim.x * kHistBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear0_words; i += stride) clear0[i] = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear1_words; i += stride) clear1[i] = 0;
     __syncthreads();
 
     const uint64_t b0 = (uint64_t)blockIdx.x * chunk;
     const uint64_t b1 = b0 + chunk < n ? b0 + chunk : n;
     auto count = [&](UK raw) {
-        const UK tk = tw_in<UK, KIND>(raw) ^ flip;
+        const UK tk = sort_key<UK, KIND, DESC>(raw);
 #pragma unroll
         for (int p = 0; p < P; ++p)
-            atomicAdd(&s_hist[((uint32_t)p * kRadix + digit_of<UK, KIND>(tk, p * kRadixBits, flip)) * C + copy], 1u);
+            atomicAdd(&s_hist[((uint32_t)p * kRadix + digit_of<UK, KIND, DESC>(tk, p * kRadixBits)) * C + copy], 1u);
     };
     constexpr uint64_t V = 16 / sizeof(UK);
     constexpr int kVecs = 4;
@@ -297,30 +329,29 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     }
     for (uint64_t i = tail + tid; i < b1; i += kHistBlock) count(keys[i]);
     __syncthreads();
-    // global adds with their results consumed: each has been performed
-    // before this workgroup's arrival below is counted
-    uint32_t seen = 0;
+    // one global add per non-zero bin (sum of the lane copies)
     for (uint32_t i = tid; i < (uint32_t)(P * kRadix); i += kHistBlock) {
         uint32_t c = 0;
 #pragma unroll 8
         for (int k = 0; k < C; ++k) c += s_hist[i * C + k];
-        if (c) seen |= __hip_atomic_fetch_add(&bins[i], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (c) __hip_atomic_fetch_add(&bins[i], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // zero the look-back state of pass 0
-    const uint64_t stride = (uint64_t)gridDim.x * kHistBlock;
-    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear0_words; i += stride) clear0[i] = 0;
-    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear1_words; i += stride) clear1[i] = 0;
 
-    // the last workgroup to arrive plans the passes (hot digits, skipped
-    // passes, buffer routing) from the finished bins
-    __shared__ uint32_t s_last, s_trivial[16];
-    if (tid == 0) s_last = 0;
+    // The last workgroup to arrive plans the passes (hot digits, skipped
+    // passes, buffer routing) from the finished bins: every workgroup's adds
+    // (and clears) are released before its arrival, and the last one
+    // acquires them all before it reads the bins.
+    // (The workgroup barrier orders every thread's adds before thread 0's
+    // release; one agent-scope fence per workgroup: fences in all 16 waves
+    // measured 16 us slower per sort, relaxed ordering no faster.)
     __syncthreads();
-    if (seen == 0xFFFFFFFFu) s_last = 2;  // (a bin below 2^32 never reads so) every add's result is awaited here
+    if (tid == 0)
+        *s_last = __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     __syncthreads();
-    if (tid == 0) s_last |= ticket(arrivals) == gridDim.x - 1 ? 1u : 0u;
-    __syncthreads();
-    if (s_last & 1u) rs_make_plan<kHistBlock>(bins, (uint32_t)P, n, hot, plan, s_trivial);
+    if (*s_last) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        rs_make_plan<kHistBlock>(bins, (uint32_t)P, n, hot, plan, s_trivial);
+    }
 }
 
 // ------------------------------------------------------------------ onesweep pass
@@ -342,11 +373,12 @@ struct OnesweepSmem {
 };
 
 // Waves per SIMD the register allocation targets: 6 (three 512-thread
-// workgroups per CU) for keys-only passes, 4 (two) when values ride along.
+// workgroups per CU) for keys-only passes and 4-byte pairs, 4 (two) when an
+// 8-byte key or value rides along.
 template <class UK, class UV, bool PAIRS>
 constexpr int os_waves_per_eu()
 {
-    return PAIRS ? 4 : 6;
+    return PAIRS && (sizeof(UK) == 8 || sizeof(UV) == 8) ? 4 : 6;
 }
 
 // Look-back state of one pass: tcount[tiles][256] (tile digit counts,
@@ -388,12 +420,12 @@ __device__ __forceinline__ uint32_t set_half16(uint32_t w, int hi, uint32_t v)
     return hi ? (w & 0xFFFFu) | (v << 16) : (w & 0xFFFF0000u) | v;
 }
 
-template <int IPT, class UK, class UV, int KIND, bool PAIRS>
+template <int IPT, class UK, class UV, int KIND, bool PAIRS, bool DESC>
 __global__ __launch_bounds__(kOsBlock)
 __attribute__((amdgpu_waves_per_eu(os_waves_per_eu<UK, UV, PAIRS>(), os_waves_per_eu<UK, UV, PAIRS>())))
 void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
-                        LbState regions, uint32_t log_run, UK flip, const uint32_t *__restrict__ hot_digits,
-                        const uint32_t *__restrict__ pass_plan)
+                        LbState regions, uint32_t log_run, const uint32_t *__restrict__ hot_digits,
+                        const uint32_t *__restrict__ pass_plan, WaitCtl ctl)
 {
     constexpr int TILE = kOsBlock * IPT;
     constexpr int HALF = TILE / 2;
@@ -430,16 +462,17 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     const LbState lb = ((plan >> kPlanRegionShift) & 1u)
                            ? LbState{regions.tcount_next, regions.bword_next, regions.tcount, regions.bword}
                            : regions;
+    const bool publish = tile != ctl.withhold;  // test hook: a withheld tile never publishes
 
     for (uint32_t i = tid; i < (uint32_t)(kOsWaves * kRadix); i += kOsBlock) (&sm.cnt[0][0])[i] = 0;
 
-    // ---- load (wave-striped), twiddle; pads are all-ones -> digit 255, last
+    // ---- load (wave-striped), sort keys; pads are all-ones -> digit 255, last
     UK tk[IPT];
     UV v[PAIRS ? IPT : 1];
     const uint32_t wbase = base + wave * WAVE_ITEMS + lane;
     if (valid == (uint32_t)TILE) {
 #pragma unroll
-        for (int u = 0; u < IPT; ++u) tk[u] = tw_in<UK, KIND>(__builtin_nontemporal_load(kin + wbase + u * kWave)) ^ flip;
+        for (int u = 0; u < IPT; ++u) tk[u] = sort_key<UK, KIND, DESC>(__builtin_nontemporal_load(kin + wbase + u * kWave));
         if constexpr (PAIRS) {
 #pragma unroll
             for (int u = 0; u < IPT; ++u) v[u] = __builtin_nontemporal_load(vin + wbase + u * kWave);
@@ -448,7 +481,7 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
 #pragma unroll
         for (int u = 0; u < IPT; ++u) {
             const uint32_t idx = wbase + u * kWave;
-            tk[u] = idx < n ? UK(tw_in<UK, KIND>(kin[idx]) ^ flip) : UK(~UK(0));
+            tk[u] = idx < n ? sort_key<UK, KIND, DESC>(kin[idx]) : UK(~UK(0));
             if constexpr (PAIRS) v[u] = idx < n ? vin[idx] : UV(0);
         }
     }
@@ -461,22 +494,24 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     // Lanes holding the pass's hot digit (skewed inputs: up to a third of the
     // keys) are represented in the instruction by their lowest lane, which
     // adds their number; the others rank by position among them.  Every key
-    // still takes one lane of one atomic instruction, in lane order.
+    // still takes one lane of one atomic instruction, in lane order.  (A
+    // separate loop for passes without a hot digit measured no faster.)
     const uint32_t hot = hot_digit;
     auto rank_of = [&](uint32_t dd) -> uint32_t {
         const bool in_hot = dd == hot;
         const uint64_t m = ballot(in_hot);
         const uint32_t leader = m ? (uint32_t)__builtin_ctzll(m) : (uint32_t)kWave;
         uint32_t res = 0;
-        if (!in_hot || lane == leader) res = atomicAdd(&cnt[dd], lane == leader ? (uint32_t)__builtin_popcountll(m) : 1u);
+        if (!in_hot || lane == leader)
+            res = atomicAdd(&cnt[dd], lane == leader ? (uint32_t)__builtin_popcountll(m) : 1u);
         if (!m) return res;
-        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)res, (int)leader);
-        return in_hot ? base + mask_rank(m) : res;
+        const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)res, (int)leader);
+        return in_hot ? b + mask_rank(m) : res;
     };
 #pragma unroll
     for (int u = 0; u < IPT; u += 2) {
-        const uint32_t r0 = rank_of(digit_of<UK, KIND>(tk[u], shift, flip));
-        const uint32_t r1 = rank_of(digit_of<UK, KIND>(tk[u + 1], shift, flip));
+        const uint32_t r0 = rank_of(digit_of<UK, KIND, DESC>(tk[u], shift));
+        const uint32_t r1 = rank_of(digit_of<UK, KIND, DESC>(tk[u + 1], shift));
         rank2[u / 2] = r0 | (r1 << 16);
         if ((u & 7) == 6) __builtin_amdgcn_sched_barrier(0);
     }
@@ -503,11 +538,13 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
             total += c;
         }
         if (d == kRadix - 1) total -= (uint32_t)TILE - valid;  // drop the pads
-        st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], total | kLbPartial);
-        // batch 0's word only ever carries its inclusive prefix
-        if (batch > 0)
-            __hip_atomic_fetch_add(&lb.bword[(size_t)batch * kRadix + d], kBwArrive + total, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        if (publish) {
+            st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], total | kLbPartial);
+            // batch 0's word only ever carries its inclusive prefix
+            if (batch > 0)
+                __hip_atomic_fetch_add(&lb.bword[(size_t)batch * kRadix + d], kBwArrive + total, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
         sm.total[d] = total;
         lb.tcount_next[(size_t)tile * kRadix + d] = 0;
         if (bpos == 0) lb.bword_next[(size_t)batch * kRadix + d] = 0;
@@ -521,10 +558,12 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     if (batch == 0) gbase = digit_excl_scan(owner ? bins[d] : 0u, sm.wsum[1]);
     __syncthreads();
 
-    // ---- tile ranks (repacked in place); first half of the sorted tile into LDS
+    // ---- tile ranks (repacked in place); first half of the sorted tile into
+    // LDS.  (Reading the wave bases of 8 keys in one burst before their stores
+    // measured slower: 2.13 against 2.07 ms per sort.)
 #pragma unroll
     for (int u = 0; u < IPT; ++u) {
-        const uint32_t dd = digit_of<UK, KIND>(tk[u], shift, flip);
+        const uint32_t dd = digit_of<UK, KIND, DESC>(tk[u], shift);
         const uint32_t r = half16(rank2[u / 2], u & 1) + sm.cnt[wave][dd];
         rank2[u / 2] = set_half16(rank2[u / 2], u & 1, r);
         if (r < (uint32_t)HALF) sm.keys[r] = tk[u];
@@ -542,11 +581,15 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
         uint32_t w7[kBatch - 1];
 #pragma unroll
         for (int k = 0; k < kBatch - 1; ++k) w7[k] = (uint32_t)k < bpos ? ld_agent32(rt, o2 + k * kRadix * 4) : 1u;
-        for (uint32_t spins = 0; spins < kSpinLimit; ++spins) {
+        for (uint32_t spins = 0;; ++spins) {
             bool all = true;
 #pragma unroll
             for (int k = 0; k < kBatch - 1; ++k) all &= w7[k] != 0;
             if (all) break;
+            if (spins >= ctl.spin_limit) {
+                report_timeout(ctl);
+                break;
+            }
             __builtin_amdgcn_s_sleep(kSleep);
             asm volatile("" ::: "memory");  // the reloads below are new reads
 #pragma unroll
@@ -567,7 +610,7 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(lb.bword, batch * kRadix * 8u);
         uint32_t acc = 0;
         int32_t j = (int32_t)batch - 1;
-        for (uint32_t spins = 0; spins < kSpinLimit; ++spins) {
+        for (uint32_t spins = 0;; ++spins) {
             uint64_t w[kWindow];
             asm volatile("" ::: "memory");  // every poll is a new read
             if (j >= kWindow - 1) {
@@ -584,33 +627,40 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
 #pragma unroll
             for (int k = 0; k < kWindow; ++k) {
                 if (!done && !stall) {
-                    uint32_t v = 0;
-                    const int st = j - k >= 0 ? batch_word_state(w[k], v) : 2;
+                    uint32_t vv = 0;
+                    const int st = j - k >= 0 ? batch_word_state(w[k], vv) : 2;
                     stall = st == 0;
                     done = st == 2;
-                    acc += v;
+                    acc += vv;
                     adv = stall ? adv : k + 1;
                 }
             }
             if (done) break;
             j -= adv;
-            if (stall) __builtin_amdgcn_s_sleep(kSleep);
+            if (stall) {
+                if (spins >= ctl.spin_limit) {
+                    report_timeout(ctl);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(kSleep);
+            }
         }
         bexcl = acc;
     }
     __syncthreads();
     if (owner) {
         const uint32_t within = sm.within[d];
-        const uint32_t incl = (bexcl + within + total) | kLbGlobal;
-        if (batch_last)
-            __hip_atomic_fetch_add(&lb.bword[(size_t)batch * kRadix + d], (uint64_t)incl << 32, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t incl = bexcl + within + total;
+        if (batch_last && publish)
+            __hip_atomic_fetch_add(&lb.bword[(size_t)batch * kRadix + d], ((uint64_t)incl << 32) | kLbGlobal,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         sm.goff[d] = bexcl + within - dexcl;
     }
     __syncthreads();
 
     // ---- write out, one half at a time: consecutive threads -> consecutive
-    // positions of a digit run; values follow with the same ranks
+    // positions of a digit run; values follow with the same ranks.  Sorted
+    // positions >= valid (the pads of the last tile) land at p >= n.
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         if (h == 1) {
@@ -629,9 +679,9 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
             const uint32_t li = j * kOsBlock + tid;
             const uint32_t i = h * HALF + li;
             const UK k = sm.keys[li];
-            const uint32_t p = i + sm.goff[digit_of<UK, KIND>(k, shift, flip)];
+            const uint32_t p = i + sm.goff[digit_of<UK, KIND, DESC>(k, shift)];
             if constexpr (PAIRS) pos[j] = p;
-            if (i < valid && p < n) kout[p] = tw_out<UK, KIND>(UK(k ^ flip));
+            if (p < n) kout[p] = raw_key<UK, KIND, DESC>(k);
             if ((j & 7) == 7) __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (PAIRS) {
@@ -645,19 +695,21 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
 #pragma unroll
             for (int j = 0; j < IPT / 2; ++j) {
                 const uint32_t li = j * kOsBlock + tid;
-                const uint32_t i = h * HALF + li;
-                if (i < valid && pos[j] < n) vout[pos[j]] = sm.vals[li];
+                if (pos[j] < n) vout[pos[j]] = sm.vals[li];
             }
         }
     }
 }
 
 // ------------------------------------------------------------------ host side
-// Items per thread: 32 (16384-key tiles) when keys and values are 4 bytes,
-// 16 (8192-key tiles) when either is 8 bytes, so a half tile of either
-// stays 32 KB.
-constexpr int os_ipt(int key_bytes, int val_bytes) { return key_bytes == 8 || val_bytes == 8 ? 16 : 32; }
+// Items per thread: 32 (16384-key tiles) for 4-byte keys alone, 16 (8192-key
+// tiles) for 8-byte keys or when values ride along (a tile's keys, values,
+// ranks and output positions then stay in registers without spilling).
+constexpr int os_ipt(int key_bytes, int val_bytes) { return key_bytes == 8 || val_bytes ? 16 : 32; }
 
+// Temp layout: status header | bins[P][256] | hot[P] | plan[P] | arrivals
+// (zeroed together by rs_init) | tile counts x 2 regions | batch words x 2
+// regions | key scratch | value scratch (pairs only).
 struct RsLayout {
     uint64_t passes, tiles, batches, bins_off, hot_off, tc_off, tc_words, bw_off, bw_words, ktmp_off, vtmp_off, total;
 };
@@ -669,23 +721,22 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     const uint64_t tile = (uint64_t)kOsBlock * os_ipt(key_bytes, val_bytes);
     L.tiles = n ? ceil_div(n, tile) : 0;
     L.batches = ceil_div(L.tiles, kBatch);
-    L.bins_off = 0;
-    L.hot_off = L.passes * kRadix * 4;  // hot digits, then the pass plan: one word each per pass
+    L.bins_off = kStatusBytes;
+    L.hot_off = L.bins_off + L.passes * kRadix * 4;  // hot digits, then the pass plan: one word each per pass
     L.tc_off = align_up(L.hot_off + (2 * L.passes + 1) * 4, 256);  // + the histogram's arrival counter
     L.tc_words = L.tiles * kRadix;
     L.bw_off = L.tc_off + align_up(2 * L.tc_words * 4, 256);
     L.bw_words = L.batches * kRadix;
     L.ktmp_off = L.bw_off + align_up(2 * L.bw_words * 8, 256);  // 64-bit words
     L.vtmp_off = L.ktmp_off + align_up(n * key_bytes, 256);
-    L.total = L.vtmp_off + align_up(n * val_bytes, 256);
+    L.total = n ? L.vtmp_off + align_up(n * val_bytes, 256) : 0;
     return L;
 }
 
-template <class UK, class UV, int KIND, bool PAIRS>
-int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const void *vin_,
-           void *vout_, uint64_t n, bool descending, hipStream_t s)
+template <class UK, class UV, int KIND, bool PAIRS, bool DESC>
+int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const void *vin_, void *vout_, uint64_t n,
+           hipStream_t s)
 {
-    const UK flip = descending ? UK(~UK(0)) : UK(0);
     constexpr int IPT = os_ipt(sizeof(UK), PAIRS ? sizeof(UV) : 0);
     if (n == 0) return LCPP_OK;
     if (n > kMaxItems) return LCPP_ERR_INVALID_ARG;
@@ -698,6 +749,7 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     if (temp_bytes < L.total) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
     char *t = static_cast<char *>(temp);
+    uint32_t *status = reinterpret_cast<uint32_t *>(t);
     uint32_t *bins = reinterpret_cast<uint32_t *>(t + L.bins_off);
     uint32_t *hot = reinterpret_cast<uint32_t *>(t + L.hot_off);
     uint32_t *plan = hot + L.passes;
@@ -709,15 +761,16 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     UV *vtmp = reinterpret_cast<UV *>(t + L.vtmp_off);
     const int P = (int)L.passes;
 
-    // bins, hot digits, plan and the histogram's arrival counter are contiguous
-    LCPP_LAUNCH("rs_init", s, rs_init_kernel<<<1, 256, 0, s>>>(bins, P * kRadix + 2 * P + 1));
+    // status header, bins, hot digits, plan and the arrival counter are contiguous
+    const uint32_t init_words = (uint32_t)((L.hot_off + (2 * L.passes + 1) * 4) / 4);
+    LCPP_LAUNCH("rs_init", s, rs_init_kernel<<<1, 256, 0, s>>>(status, init_words));
     LCPP_CHECK_LAUNCH();
     {
         // one 1024-thread workgroup per CU (128 KB of LDS each)
         constexpr size_t lds = hist_lds_bytes<UK>();
         static DeviceCache lds_set;
         if (device_cached(lds_set, [] {
-                return hipFuncSetAttribute(reinterpret_cast<const void *>(&rs_histogram_kernel<UK, KIND>),
+                return hipFuncSetAttribute(reinterpret_cast<const void *>(&rs_histogram_kernel<UK, KIND, DESC>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess
                            ? 1
                            : -1;
@@ -730,8 +783,8 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         const uint64_t chunk = ceil_div(htiles, grid) * htile;
         grid = ceil_div(n, chunk);
         LCPP_LAUNCH("rs_histogram", s,
-                    rs_histogram_kernel<UK, KIND><<<(uint32_t)grid, kHistBlock, lds, s>>>(
-                        kin, n, chunk, bins, tc[0], L.tc_words, reinterpret_cast<uint32_t *>(bw[0]), 2 * L.bw_words, flip,
+                    rs_histogram_kernel<UK, KIND, DESC><<<(uint32_t)grid, kHistBlock, lds, s>>>(
+                        kin, n, chunk, bins, tc[0], L.tc_words, reinterpret_cast<uint32_t *>(bw[0]), 2 * L.bw_words,
                         plan + P, hot, plan));
         LCPP_CHECK_LAUNCH();
     }
@@ -740,8 +793,8 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     const int lr1 = device_cached(run_cache, [] {
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, reinterpret_cast<const void *>(&rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS>), kOsBlock,
-                0) != hipSuccess)
+                &per_cu, reinterpret_cast<const void *>(&rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC>),
+                kOsBlock, 0) != hipSuccess)
             return -1;
         const uint64_t resident = (uint64_t)(per_cu > 0 ? per_cu : 1) * (uint64_t)device_cus();
         int lr = 0;
@@ -750,14 +803,15 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     });
     if (lr1 < 0) return LCPP_ERR_HIP;
     const uint32_t log_run = (uint32_t)(lr1 - 1);
+    const WaitCtl ctl = wait_ctl(status);
     // buffers and look-back regions per pass come from the device-side plan
     const RsBuffers<UK, UV> buf{kin, ktmp, kout, vin, vtmp, vout};
     const LbState regions{tc[0], bw[0], tc[1], bw[1]};
     for (int p = 0; p < P; ++p) {
         LCPP_LAUNCH("rs_onesweep", s,
-                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
-                        buf, (uint32_t)n, (uint32_t)(p * kRadixBits), bins + p * kRadix, regions, log_run, flip,
-                        hot + p, plan + p)));
+                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
+                        buf, (uint32_t)n, (uint32_t)(p * kRadixBits), bins + p * kRadix, regions, log_run,
+                        hot + p, plan + p, ctl)));
         LCPP_CHECK_LAUNCH();
     }
     return LCPP_OK;
@@ -781,16 +835,23 @@ int dtype_bytes(lcpp_dtype t)
     }
 }
 
-template <class UK, class UV, bool PAIRS>
-int rs_kind_dispatch(int kind, void *temp, size_t tb, const void *ki, void *ko, const void *vi,
-                     void *vo, uint64_t n, bool desc, hipStream_t s)
+template <class UK, class UV, bool PAIRS, bool DESC>
+int rs_kind_dispatch(int kind, void *temp, size_t tb, const void *ki, void *ko, const void *vi, void *vo, uint64_t n,
+                     hipStream_t s)
 {
     switch (kind) {
-    case kUnsigned: return rs_run<UK, UV, kUnsigned, PAIRS>(temp, tb, ki, ko, vi, vo, n, desc, s);
-    case kSigned: return rs_run<UK, UV, kSigned, PAIRS>(temp, tb, ki, ko, vi, vo, n, desc, s);
-    case kFloat: return rs_run<UK, UV, kFloat, PAIRS>(temp, tb, ki, ko, vi, vo, n, desc, s);
+    case kUnsigned: return rs_run<UK, UV, kUnsigned, PAIRS, DESC>(temp, tb, ki, ko, vi, vo, n, s);
+    case kSigned: return rs_run<UK, UV, kSigned, PAIRS, DESC>(temp, tb, ki, ko, vi, vo, n, s);
+    case kFloat: return rs_run<UK, UV, kFloat, PAIRS, DESC>(temp, tb, ki, ko, vi, vo, n, s);
     default: return LCPP_ERR_UNSUPPORTED_DTYPE;
     }
+}
+template <class UK, class UV, bool PAIRS>
+int rs_order_dispatch(bool desc, int kind, void *temp, size_t tb, const void *ki, void *ko, const void *vi, void *vo,
+                      uint64_t n, hipStream_t s)
+{
+    return desc ? rs_kind_dispatch<UK, UV, PAIRS, true>(kind, temp, tb, ki, ko, vi, vo, n, s)
+                : rs_kind_dispatch<UK, UV, PAIRS, false>(kind, temp, tb, ki, ko, vi, vo, n, s);
 }
 
 }  // namespace
@@ -825,10 +886,10 @@ int sort_keys(lcpp_dtype k, void *temp, size_t tb, const void *keys_in, void *ke
     const int kind = key_kind(k);
     if (kind < 0) return LCPP_ERR_UNSUPPORTED_DTYPE;
     if (dtype_bytes(k) == 4)
-        return rs_kind_dispatch<uint32_t, uint32_t, false>(kind, temp, tb, keys_in, keys_out, nullptr, nullptr, n,
-                                                           desc, s);
-    return rs_kind_dispatch<uint64_t, uint32_t, false>(kind, temp, tb, keys_in, keys_out, nullptr, nullptr, n,
-                                                       desc, s);
+        return rs_order_dispatch<uint32_t, uint32_t, false>(desc, kind, temp, tb, keys_in, keys_out, nullptr, nullptr,
+                                                            n, s);
+    return rs_order_dispatch<uint64_t, uint32_t, false>(desc, kind, temp, tb, keys_in, keys_out, nullptr, nullptr, n,
+                                                        s);
 }
 
 int sort_pairs(lcpp_dtype k, lcpp_dtype v, void *temp, size_t tb, const void *keys_in, void *keys_out,
@@ -839,16 +900,16 @@ int sort_pairs(lcpp_dtype k, lcpp_dtype v, void *temp, size_t tb, const void *ke
     const int kb = dtype_bytes(k), vb = dtype_bytes(v);
     if (kind < 0 || !vb) return LCPP_ERR_UNSUPPORTED_DTYPE;
     if (kb == 4 && vb == 4)
-        return rs_kind_dispatch<uint32_t, uint32_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
-                                                          desc, s);
+        return rs_order_dispatch<uint32_t, uint32_t, true>(desc, kind, temp, tb, keys_in, keys_out, vals_in, vals_out,
+                                                           n, s);
     if (kb == 4 && vb == 8)
-        return rs_kind_dispatch<uint32_t, uint64_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
-                                                          desc, s);
+        return rs_order_dispatch<uint32_t, uint64_t, true>(desc, kind, temp, tb, keys_in, keys_out, vals_in, vals_out,
+                                                           n, s);
     if (kb == 8 && vb == 4)
-        return rs_kind_dispatch<uint64_t, uint32_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
-                                                          desc, s);
-    return rs_kind_dispatch<uint64_t, uint64_t, true>(kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
-                                                      desc, s);
+        return rs_order_dispatch<uint64_t, uint32_t, true>(desc, kind, temp, tb, keys_in, keys_out, vals_in, vals_out,
+                                                           n, s);
+    return rs_order_dispatch<uint64_t, uint64_t, true>(desc, kind, temp, tb, keys_in, keys_out, vals_in, vals_out, n,
+                                                       s);
 }
 }  // namespace
 

@@ -7,11 +7,11 @@
 // common/thread_operators.h:19-47 (ArgMaxOp/ArgMinOp).
 //
 // MI355X design: one streaming pass.  A grid of at most 512 workgroups
-// (2048 for ArgMin/ArgMax) partitions the input into equal contiguous chunks
-// whose length is a multiple of the tile (128 KiB; 32 KiB for Arg*), so
+// (1024 for ArgMin/ArgMax) partitions the input into equal contiguous chunks
+// whose length is a multiple of the tile (128 KiB; 48 KiB for Arg*), so
 // every workgroup's range is exact (the reference dispatches more blocks
 // than it partitions for N > 10,485,760 and reads past the end).  Each thread
-// streams 16-byte vectors (32 per tile; 8 for Arg*), folds them in
+// streams 16-byte vectors (32 per tile; 12 for Arg*), folds them in
 // registers, the workgroup folds its four wave totals, and one partial per
 // workgroup lands in temp storage.  A
 // one-workgroup kernel folds the partials in a fixed order, so the float
@@ -174,10 +174,11 @@ template <class T, class Op, class Xf>
 __global__ __launch_bounds__(kRedBlock) void reduce_partials_kernel(const T *__restrict__ in,
                                                                     uint64_t n, uint64_t chunk,
                                                                     T *__restrict__ partials,
-                                                                    T init, int direct)
+                                                                    T init, int direct, uint32_t *status)
 {
     Op op;
     Xf xf;
+    if (status && blockIdx.x == 0 && threadIdx.x == 0) *status = 0;  // nothing here waits
     T acc = Op::template identity<T>();
     const uint64_t b0 = (uint64_t)blockIdx.x * chunk;
     const uint64_t b1 = b0 + chunk < n ? b0 + chunk : n;
@@ -206,9 +207,10 @@ __global__ __launch_bounds__(kRedBlock) void reduce_partials_kernel(const T *__r
 template <class T, class Op>
 __global__ __launch_bounds__(kRedBlock) void reduce_final_kernel(const T *__restrict__ partials,
                                                                  uint32_t count,
-                                                                 T *__restrict__ out, T init)
+                                                                 T *__restrict__ out, T init, uint32_t *status)
 {
     Op op;
+    if (status && threadIdx.x == 0) *status = 0;
     T acc = Op::template identity<T>();
     for (uint32_t i = threadIdx.x; i < count; i += kRedBlock) acc = op(acc, partials[i]);
     acc = block_reduce(acc, op);
@@ -219,7 +221,7 @@ template <class T>
 uint64_t reduce_temp(uint64_t n)
 {
     RedGrid g = red_grid<T, false>(n);
-    return g.grid > 1 ? align_up((uint64_t)g.grid * sizeof(T), 256) : 0;
+    return g.grid > 1 ? kStatusBytes + align_up((uint64_t)g.grid * sizeof(T), 256) : 0;
 }
 
 template <class T, class Op, class Xf>
@@ -231,25 +233,30 @@ int reduce_launch(void *temp, size_t temp_bytes, const void *in_, void *out_, ui
     if (!out || (n && !in)) return LCPP_ERR_INVALID_ARG;
     RedGrid g = red_grid<T, false>(n);
     if (g.grid == 1) {
-        // one workgroup writes op(init, fold) itself
+        // one workgroup writes op(init, fold) itself; a temp buffer, if one
+        // is passed, only has its status word cleared
+        uint32_t *st = temp && temp_bytes >= kStatusBytes && !(reinterpret_cast<uintptr_t>(temp) & 255)
+                           ? static_cast<uint32_t *>(temp)
+                           : nullptr;
         if (n == 0) {
             LCPP_LAUNCH("reduce_final", s,
-                        (reduce_final_kernel<T, Op><<<1, kRedBlock, 0, s>>>(out, 0, out, init)));
+                        (reduce_final_kernel<T, Op><<<1, kRedBlock, 0, s>>>(out, 0, out, init, st)));
         } else {
             LCPP_LAUNCH("reduce_partials", s,
-                        (reduce_partials_kernel<T, Op, Xf><<<1, kRedBlock, 0, s>>>(in, n, g.chunk, out, init, 1)));
+                        (reduce_partials_kernel<T, Op, Xf><<<1, kRedBlock, 0, s>>>(in, n, g.chunk, out, init, 1, st)));
         }
         LCPP_CHECK_LAUNCH();
         return LCPP_OK;
     }
     if (temp_bytes < reduce_temp<T>(n)) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
-    T *partials = static_cast<T *>(temp);
+    T *partials = reinterpret_cast<T *>(static_cast<char *>(temp) + kStatusBytes);
     LCPP_LAUNCH("reduce_partials", s,
-                (reduce_partials_kernel<T, Op, Xf><<<g.grid, kRedBlock, 0, s>>>(in, n, g.chunk, partials, init, 0)));
+                (reduce_partials_kernel<T, Op, Xf><<<g.grid, kRedBlock, 0, s>>>(
+                    in, n, g.chunk, partials, init, 0, static_cast<uint32_t *>(temp))));
     LCPP_CHECK_LAUNCH();
     LCPP_LAUNCH("reduce_final", s,
-                (reduce_final_kernel<T, Op><<<1, kRedBlock, 0, s>>>(partials, g.grid, out, init)));
+                (reduce_final_kernel<T, Op><<<1, kRedBlock, 0, s>>>(partials, g.grid, out, init, nullptr)));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
 }
@@ -275,11 +282,13 @@ __global__ __launch_bounds__(kRedBlock) void arg_partials_kernel(const T *__rest
                                                                  uint64_t chunk,
                                                                  IdxVal<T> *__restrict__ partials,
                                                                  T *__restrict__ out,
-                                                                 uint32_t *__restrict__ out_index)
+                                                                 uint32_t *__restrict__ out_index,
+                                                                 uint32_t *status)
 {
     using P = IdxVal<T>;
     ArgOp<IS_MAX> op;
     P acc = ArgOp<IS_MAX>::template identity<T>();
+    if (status && blockIdx.x == 0 && threadIdx.x == 0) *status = 0;  // nothing here waits
     const uint64_t b0 = (uint64_t)blockIdx.x * chunk;
     const uint64_t b1 = b0 + chunk < n ? b0 + chunk : n;
     const uint32_t tid = threadIdx.x;
@@ -320,10 +329,11 @@ __global__ __launch_bounds__(kRedBlock) void arg_partials_kernel(const T *__rest
 template <class T, bool IS_MAX>
 __global__ __launch_bounds__(kRedBlock) void arg_final_kernel(const IdxVal<T> *__restrict__ partials,
                                                               uint32_t count, T *__restrict__ out,
-                                                              uint32_t *__restrict__ out_index)
+                                                              uint32_t *__restrict__ out_index, uint32_t *status)
 {
     using P = IdxVal<T>;
     ArgOp<IS_MAX> op;
+    if (status && threadIdx.x == 0) *status = 0;
     P acc = ArgOp<IS_MAX>::template identity<T>();
     for (uint32_t i = threadIdx.x; i < count; i += kRedBlock) acc = op(acc, partials[i]);
     acc = block_reduce_pair(acc, op);
@@ -337,7 +347,7 @@ template <class T>
 uint64_t arg_temp(uint64_t n)
 {
     RedGrid g = red_grid<T, true>(n);
-    return g.grid > 1 ? align_up((uint64_t)g.grid * sizeof(IdxVal<T>), 256) : 0;
+    return g.grid > 1 ? kStatusBytes + align_up((uint64_t)g.grid * sizeof(IdxVal<T>), 256) : 0;
 }
 
 template <class T, bool IS_MAX>
@@ -350,22 +360,29 @@ int arg_launch(void *temp, size_t temp_bytes, const void *in_, void *out_, uint3
     if (n > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;  // 32-bit indices, as the reference
     RedGrid g = red_grid<T, true>(n);
     if (g.grid == 1) {
+        uint32_t *st = temp && temp_bytes >= kStatusBytes && !(reinterpret_cast<uintptr_t>(temp) & 255)
+                           ? static_cast<uint32_t *>(temp)
+                           : nullptr;
         if (n == 0) {
-            LCPP_LAUNCH("arg_final", s, (arg_final_kernel<T, IS_MAX><<<1, kRedBlock, 0, s>>>(nullptr, 0, out, out_index)));
+            LCPP_LAUNCH("arg_final", s,
+                        (arg_final_kernel<T, IS_MAX><<<1, kRedBlock, 0, s>>>(nullptr, 0, out, out_index, st)));
         } else {
             LCPP_LAUNCH("arg_partials", s,
-                        (arg_partials_kernel<T, IS_MAX><<<1, kRedBlock, 0, s>>>(in, n, g.chunk, nullptr, out, out_index)));
+                        (arg_partials_kernel<T, IS_MAX><<<1, kRedBlock, 0, s>>>(in, n, g.chunk, nullptr, out, out_index,
+                                                                                  st)));
         }
         LCPP_CHECK_LAUNCH();
         return LCPP_OK;
     }
     if (temp_bytes < arg_temp<T>(n)) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
-    IdxVal<T> *partials = static_cast<IdxVal<T> *>(temp);
+    IdxVal<T> *partials = reinterpret_cast<IdxVal<T> *>(static_cast<char *>(temp) + kStatusBytes);
     LCPP_LAUNCH("arg_partials", s,
-                (arg_partials_kernel<T, IS_MAX><<<g.grid, kRedBlock, 0, s>>>(in, n, g.chunk, partials, nullptr, nullptr)));
+                (arg_partials_kernel<T, IS_MAX><<<g.grid, kRedBlock, 0, s>>>(in, n, g.chunk, partials, nullptr, nullptr,
+                                                                             static_cast<uint32_t *>(temp))));
     LCPP_CHECK_LAUNCH();
-    LCPP_LAUNCH("arg_final", s, (arg_final_kernel<T, IS_MAX><<<1, kRedBlock, 0, s>>>(partials, g.grid, out, out_index)));
+    LCPP_LAUNCH("arg_final", s,
+                (arg_final_kernel<T, IS_MAX><<<1, kRedBlock, 0, s>>>(partials, g.grid, out, out_index, nullptr)));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
 }

@@ -36,8 +36,8 @@ RbkLayout<V> rbk_layout(uint64_t n)
 {
     RbkLayout<V> L{};
     L.tiles = bk_tiles<V>(n);
-    L.cwords_off = 0;
-    L.vwords_off = align_up(L.tiles * 8, 256);
+    L.cwords_off = kStatusBytes;  // after the status header
+    L.vwords_off = L.cwords_off + align_up(L.tiles * 8, 256);
     L.total = L.vwords_off + align_up(L.tiles * 8 * lb_words<V>(), 256);
     return L;
 }
@@ -50,7 +50,8 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
                                                                  K *__restrict__ unique_out,
                                                                  V *__restrict__ agg_out,
                                                                  uint32_t *__restrict__ num_runs, uint32_t n,
-                                                                 uint64_t *cwords, uint64_t *vwords, int vec_ok)
+                                                                 uint64_t *cwords, uint64_t *vwords, int vec_ok,
+                                                                 WaitCtl ctl)
 {
     constexpr int VP = bk_vp<V>();
     constexpr uint32_t TILE = bk_tile<V>();
@@ -105,7 +106,7 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
         for (int k = 0; k < kBkVecs; ++k)
 #pragma unroll
             for (int w = 0; w < kBkWaves; ++w) tcount += s_C[k][w];
-        if (lane == 0) lb_publish(cwords, tile, tcount, tile == 0 ? kStInclusive : kStPartial);
+        if (lane == 0) lb_publish(cwords, tile, tcount, tile == 0 ? kStInclusive : kStPartial, ctl);
     }
 
     // pass 1: per vector, (has-head, open fold) pairs, their wave scan, wave
@@ -142,13 +143,13 @@ __global__ __launch_bounds__(kBkBlock) void reduce_by_key_kernel(const K *__rest
             for (int w = 0; w < kBkWaves; ++w) seg_fold(tf, ts, ((s_F[k] >> w) & 1u) != 0, s_S[k][w], op);
         // always wait: a head at the tile's first element closes the run the
         // previous tile left open, whose aggregate is exactly this prefix
-        const V p = lb_segmented_tile(vwords, tile, ts, tf, true, op, ident);
+        const V p = lb_segmented_tile(vwords, tile, ts, tf, true, op, ident, ctl);
         if (lane == 0) s_vprefix = p;
     } else if (wave == 1) {
         uint32_t p = 0;
         if (tile > 0) {
-            p = lb_wait_prefix(cwords, tile, SumOp(), 0u);
-            if (lane == 0) lb_publish(cwords, tile, p + tcount, kStInclusive);
+            p = lb_wait_prefix(cwords, tile, SumOp(), 0u, ctl);
+            if (lane == 0) lb_publish(cwords, tile, p + tcount, kStInclusive, ctl);
         }
         if (lane == 0) s_cprefix = p;
     }
@@ -229,12 +230,15 @@ int rbk_launch(void *temp, size_t tb, const void *keys_, const void *in_, void *
     char *t = static_cast<char *>(temp);
     uint64_t *cwords = reinterpret_cast<uint64_t *>(t + L.cwords_off);
     uint64_t *vwords = reinterpret_cast<uint64_t *>(t + L.vwords_off);
-    // both regions are contiguous up to alignment padding: one fill
-    if (lb_init(cwords, (L.total - L.cwords_off) / 8, s, "reduce_by_key_init") != LCPP_OK) return LCPP_ERR_HIP;
+    // the status header and both regions are contiguous up to alignment
+    // padding: one fill
+    if (lb_init(reinterpret_cast<uint64_t *>(t), L.total / 8, s, "reduce_by_key_init") != LCPP_OK)
+        return LCPP_ERR_HIP;
+    const WaitCtl ctl = wait_ctl(reinterpret_cast<uint32_t *>(t));
     const int vec_ok = ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(in)) & 15) == 0;
     LCPP_LAUNCH("reduce_by_key", s,
                 (reduce_by_key_kernel<K, V, Op><<<(uint32_t)L.tiles, kBkBlock, 0, s>>>(
-                    keys, in, uk, agg, num_runs, (uint32_t)n, cwords, vwords, vec_ok)));
+                    keys, in, uk, agg, num_runs, (uint32_t)n, cwords, vwords, vec_ok, ctl)));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
 }

@@ -1,8 +1,11 @@
-// runtime.hip — status strings, version and launch instrumentation.
+// runtime.hip — status strings, version, the device status word, test
+// hooks and launch instrumentation.
 //
 // Reference: runtime/core.h:35-112 (lazy JIT compile + memo, lcpp_check).
 // Here every kernel is compiled ahead of time for gfx950, so there is no JIT
-// cache; the C ABI returns status codes instead of asserting.
+// cache; the C ABI returns status codes instead of asserting, and the
+// debug-stream check (commit, synchronize, assert) becomes lcpp_temp_status:
+// synchronize, then read the status word the call's kernels wrote.
 #include <atomic>
 #include <mutex>
 #include <string>
@@ -34,7 +37,17 @@ struct Open {
     hipStream_t stream;
 };
 
+// lcpp_test_set_lookback_fault: read by every launch that waits
+std::atomic<uint32_t> g_withhold{0xFFFFFFFFu};
+std::atomic<uint32_t> g_spin_limit{0};
+
 }  // namespace
+
+WaitCtl wait_ctl(uint32_t *status)
+{
+    const uint32_t lim = g_spin_limit.load(std::memory_order_relaxed);
+    return WaitCtl{status, lim ? lim : kSpinLimit, g_withhold.load(std::memory_order_relaxed)};
+}
 
 LaunchScope::LaunchScope(const char *name, hipStream_t s) : rec(nullptr)
 {
@@ -77,8 +90,36 @@ extern "C" const char *lcpp_status_string(int status)
     case LCPP_ERR_TEMP_TOO_SMALL: return "LCPP_ERR_TEMP_TOO_SMALL";
     case LCPP_ERR_UNSUPPORTED_DTYPE: return "LCPP_ERR_UNSUPPORTED_DTYPE";
     case LCPP_ERR_HIP: return "LCPP_ERR_HIP";
+    case LCPP_ERR_LOOKBACK_TIMEOUT: return "LCPP_ERR_LOOKBACK_TIMEOUT";
     default: return "LCPP_ERR_UNKNOWN";
     }
+}
+
+extern "C" int lcpp_device_status_decode(uint32_t word)
+{
+    return (word & LCPP_DEVICE_STATUS_LOOKBACK_TIMEOUT) ? LCPP_ERR_LOOKBACK_TIMEOUT : LCPP_OK;
+}
+
+extern "C" int lcpp_stream_sync(void *stream)
+{
+    return hipStreamSynchronize(static_cast<hipStream_t>(stream)) == hipSuccess ? LCPP_OK : LCPP_ERR_HIP;
+}
+
+extern "C" int lcpp_temp_status(const void *temp, size_t temp_bytes, void *stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!temp || temp_bytes < kStatusBytes) return lcpp_stream_sync(stream);
+    uint32_t word = 0;
+    if (hipMemcpyAsync(&word, temp, sizeof(word), hipMemcpyDeviceToHost, s) != hipSuccess) return LCPP_ERR_HIP;
+    if (hipStreamSynchronize(s) != hipSuccess) return LCPP_ERR_HIP;
+    return lcpp_device_status_decode(word);
+}
+
+extern "C" int lcpp_test_set_lookback_fault(uint32_t withhold_tile, uint32_t spin_limit)
+{
+    g_withhold.store(withhold_tile, std::memory_order_relaxed);
+    g_spin_limit.store(spin_limit, std::memory_order_relaxed);
+    return LCPP_OK;
 }
 
 static void drop_pending_locked()

@@ -54,8 +54,9 @@ constexpr uint32_t scan_tile()
     return kScanBlock * scan_vecs<T, INCLUSIVE>() * (16 / sizeof(T));
 }
 
-// Temp layout: packed look-back words, 8 bytes per tile (32-bit T) or 16
-// bytes per tile (64-bit T). The query covers the smaller of the two tiles.
+// Temp layout: the status header, then packed look-back words, 8 bytes per
+// tile (32-bit T) or 16 bytes per tile (64-bit T).  The query covers the
+// smaller of the two tiles.
 template <class T, bool INCLUSIVE>
 uint64_t scan_tiles(uint64_t n)
 {
@@ -65,7 +66,7 @@ template <class T>
 uint64_t scan_temp_bytes(uint64_t n)
 {
     const uint64_t tiles = std::max(scan_tiles<T, false>(n), scan_tiles<T, true>(n));
-    return align_up(tiles * (sizeof(T) == 4 ? 8 : 16), 256);
+    return tiles ? kStatusBytes + align_up(tiles * (sizeof(T) == 4 ? 8 : 16), 256) : 0;
 }
 
 // 4-byte integer kernels are held to 128 VGPRs (4 workgroups per SIMD):
@@ -82,7 +83,7 @@ template <class T, bool INCLUSIVE>
 __global__ __launch_bounds__(kScanBlock) __attribute__((amdgpu_waves_per_eu(scan_min_waves<T, INCLUSIVE>())))
 void scan_kernel(const T *__restrict__ in,
                                                           T *__restrict__ out, uint64_t n,
-                                                          uint64_t *words, int vec_ok)
+                                                          uint64_t *words, int vec_ok, WaitCtl ctl)
 {
     constexpr int V = 16 / sizeof(T);
     constexpr int K = scan_vecs<T, INCLUSIVE>();
@@ -146,7 +147,7 @@ void scan_kernel(const T *__restrict__ in,
         for (int k = 0; k < K; ++k)
 #pragma unroll
             for (int w = 0; w < W; ++w) agg = op(agg, s_wtot[k][w]);
-        const T ex = lb_scan_tile(words, tile, agg, op, T(0));
+        const T ex = lb_scan_tile(words, tile, agg, op, T(0), ctl);
         if (lane == 0) s_prefix = ex;
     }
     __syncthreads();
@@ -190,16 +191,18 @@ int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, 
     if (tiles > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;
     if (temp_bytes < scan_temp_bytes<T>(n)) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
-    uint64_t *words = static_cast<uint64_t *>(temp);
+    uint64_t *head = static_cast<uint64_t *>(temp);  // status header, then the look-back words
+    uint64_t *words = head + kStatusBytes / 8;
     const uint64_t nwords = tiles * (sizeof(T) == 4 ? 1 : 2);
-    if (lb_init(words, nwords, s, "scan_init") != LCPP_OK) return LCPP_ERR_HIP;
+    if (lb_init(head, kStatusBytes / 8 + nwords, s, "scan_init") != LCPP_OK) return LCPP_ERR_HIP;
+    const WaitCtl ctl = wait_ctl(static_cast<uint32_t *>(temp));
     const int vec_ok = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     if (inclusive)
         LCPP_LAUNCH("scan_inclusive", s,
-                    scan_kernel<T, true><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok));
+                    scan_kernel<T, true><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
     else
         LCPP_LAUNCH("scan_exclusive", s,
-                    scan_kernel<T, false><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok));
+                    scan_kernel<T, false><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
 }

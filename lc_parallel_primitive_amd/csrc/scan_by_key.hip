@@ -23,14 +23,16 @@ namespace {
 template <class V>
 uint64_t sbk_temp_bytes(uint64_t n)
 {
-    return align_up(bk_tiles<V>(n) * 8 * lb_words<V>(), 256);
+    const uint64_t tiles = bk_tiles<V>(n);
+    return tiles ? kStatusBytes + align_up(tiles * 8 * lb_words<V>(), 256) : 0;  // status header, look-back words
 }
 
 template <class K, class V, class Op, bool INCLUSIVE>
 __global__ __launch_bounds__(kBkBlock) void scan_by_key_kernel(const K *__restrict__ keys,
                                                                const V *__restrict__ vin,
                                                                V *__restrict__ vout, uint64_t n,
-                                                               uint64_t *words, V init, int vec_ok)
+                                                               uint64_t *words, V init, int vec_ok,
+                                                               WaitCtl ctl)
 {
     constexpr int VP = bk_vp<V>();
     constexpr uint32_t TILE = bk_tile<V>();
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(kBkBlock) void scan_by_key_kernel(const K *__restri
         for (int k = 0; k < kBkVecs; ++k)
 #pragma unroll
             for (int w = 0; w < kBkWaves; ++w) seg_fold(tf, ts, ((s_F[k] >> w) & 1u) != 0, s_S[k][w], op);
-        const V p = lb_segmented_tile(words, tile, ts, tf, s_first_head == 0, op, ident);
+        const V p = lb_segmented_tile(words, tile, ts, tf, s_first_head == 0, op, ident, ctl);
         if (lane == 0) s_prefix = p;
     }
     __syncthreads();
@@ -147,18 +149,21 @@ int sbk_launch(bool inclusive, void *temp, size_t tb, const void *keys_, const v
     V init;
     if (init_) memcpy(&init, init_, sizeof(V));
     else init = V(0);
-    uint64_t *words = static_cast<uint64_t *>(temp);
-    if (lb_init(words, tiles * lb_words<V>(), s, "scan_by_key_init") != LCPP_OK) return LCPP_ERR_HIP;
+    uint64_t *head = static_cast<uint64_t *>(temp);  // status header, then the look-back words
+    uint64_t *words = head + kStatusBytes / 8;
+    if (lb_init(head, kStatusBytes / 8 + tiles * lb_words<V>(), s, "scan_by_key_init") != LCPP_OK)
+        return LCPP_ERR_HIP;
+    const WaitCtl ctl = wait_ctl(static_cast<uint32_t *>(temp));
     const int vec_ok = ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(in) |
                          reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     if (inclusive)
         LCPP_LAUNCH("scan_by_key_inclusive", s,
                     (scan_by_key_kernel<K, V, Op, true><<<(uint32_t)tiles, kBkBlock, 0, s>>>(keys, in, out, n, words,
-                                                                                            init, vec_ok)));
+                                                                                            init, vec_ok, ctl)));
     else
         LCPP_LAUNCH("scan_by_key_exclusive", s,
                     (scan_by_key_kernel<K, V, Op, false><<<(uint32_t)tiles, kBkBlock, 0, s>>>(keys, in, out, n, words,
-                                                                                             init, vec_ok)));
+                                                                                             init, vec_ok, ctl)));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
 }

@@ -44,6 +44,12 @@ def lib() -> ctypes.CDLL:
         L.lcpp_copy_probe_u32.argtypes = [vp, vp, u64, vp]
         L.lcpp_gen_segments_host.restype = i
         L.lcpp_gen_segments_host.argtypes = [u64, u64, u64, u64, vp, vp]
+        L.lcpp_dg_sorted_hash_u32.restype = i
+        L.lcpp_dg_sorted_hash_u32.argtypes = [vp, u64, vp, vp]
+        L.lcpp_dg_check_stable_pairs_u32.restype = i
+        L.lcpp_dg_check_stable_pairs_u32.argtypes = [vp, vp, vp, u64, vp, vp]
+        L.lcpp_dg_lds_order_probe.restype = i
+        L.lcpp_dg_lds_order_probe.argtypes = [u64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp, vp]
         _lib = L
     return _lib
 
@@ -154,3 +160,38 @@ def copy_probe(src, dst):
     n = src.numel()
     _run(lib().lcpp_copy_probe_u32(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), n, _stream()),
          "copy_probe")
+
+
+# ---------------------------------------------------------------- device-side checkers (tests)
+def sorted_hash_u32(t):
+    """(descents, sum mod 2^64, sum of mix64 mod 2^64) of a uint32 device
+    tensor: descents == 0 means sorted; the sums are equal for equal multisets."""
+    import torch
+
+    out = torch.zeros(3, dtype=torch.uint64, device=t.device)
+    _run(lib().lcpp_dg_sorted_hash_u32(ctypes.c_void_p(t.data_ptr()), t.numel(), ctypes.c_void_p(out.data_ptr()),
+                                       _stream()), "sorted_hash_u32")
+    h = out.cpu().view(torch.int64).tolist()
+    return tuple(x & 0xFFFFFFFFFFFFFFFF for x in h)
+
+
+def check_stable_pairs_u32(keys_in, keys_out, vals_out) -> int:
+    """Bad positions of a stable uint32/uint32 sort whose values were the input
+    indices (0 <=> keys_out/vals_out is exactly the stable sort)."""
+    import torch
+
+    bad = torch.zeros(1, dtype=torch.uint64, device=keys_in.device)
+    _run(lib().lcpp_dg_check_stable_pairs_u32(ctypes.c_void_p(keys_in.data_ptr()), ctypes.c_void_p(keys_out.data_ptr()),
+                                              ctypes.c_void_p(vals_out.data_ptr()), keys_in.numel(),
+                                              ctypes.c_void_p(bad.data_ptr()), _stream()), "check_stable_pairs_u32")
+    return int(bad.cpu().view(torch.int64).item())
+
+
+def lds_order_probe(seed: int, pattern: int, waves: int, rounds: int) -> int:
+    """Lanes whose returning LDS atomic add broke lane order (see datagen.hip)."""
+    import torch
+
+    v = torch.zeros(1, dtype=torch.uint64, device="cuda")
+    _run(lib().lcpp_dg_lds_order_probe(seed, pattern, waves, rounds, ctypes.c_void_p(v.data_ptr()), _stream()),
+         "lds_order_probe")
+    return int(v.cpu().view(torch.int64).item())

@@ -67,16 +67,35 @@ def _query(fn, *args) -> int:
     return out.value
 
 
-class DeviceReduce:
-    """device/device_reduce.h:37-348 (Sum / Min / Max / ArgMin / ArgMax / ReduceByKey / TransformReduce)."""
+class _Module:
+    """What every module shares.  The geometry arguments are accepted for source
+    compatibility (the library fixes it per dtype, tuned for gfx950).
+
+    create(device, debug_stream) follows the reference's modules, whose
+    lcpp_check commits, synchronizes and asserts after each step when a debug
+    stream is given (runtime/core.h:56-64): here every call is then
+    synchronized and the device status word of its temp storage is read
+    (lcpp_temp_status), so a look-back wait that gave up raises LcppError
+    (LCPP_ERR_LOOKBACK_TIMEOUT) at the call that caused it.  Without a debug
+    stream no call synchronizes."""
 
     def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
-        # geometry is fixed per dtype inside the library (tuned for gfx950);
-        # the arguments are accepted for source compatibility
         self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
+        self._debug = False
 
     def create(self, device=None, debug_stream=None):
+        self._debug = debug_stream is not None
         return self
+
+    def _check(self, status: int, what: str, temp, stream) -> None:
+        check(status, what)
+        if self._debug:
+            check(lib().lcpp_temp_status(_ptr(temp), _nbytes(temp), _stream(stream)), what + " (device status)")
+
+
+class DeviceReduce(_Module):
+    """device/device_reduce.h:37-348 (Sum / Min / Max / ArgMin / ArgMax / ReduceByKey / TransformReduce)."""
+
 
     @staticmethod
     def GetTempStorageBytes(dtype, num_item: int) -> int:
@@ -86,8 +105,8 @@ class DeviceReduce:
         _need(d_in, num_item, "d_in")
         _need(d_out, 1, "d_out")
         _same_dtype(d_in, d_out, fn.__name__)
-        check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), num_item,
-                 _stream(stream)), fn.__name__)
+        self._check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), num_item,
+                 _stream(stream)), fn.__name__, temp, stream)
 
     def Sum(self, temp_storage, d_in, d_out, num_item: int, stream=None):
         self._run(lib().lcpp_reduce_sum, temp_storage, d_in, d_out, num_item, stream)
@@ -109,8 +128,8 @@ class DeviceReduce:
         _same_dtype(d_in, d_out, fn.__name__)
         if d_index_out.element_size() != 4:
             raise TypeError(f"{fn.__name__}: d_index_out must hold 32-bit indices")
-        check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
-                 num_item, _stream(stream)), fn.__name__)
+        self._check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
+                 num_item, _stream(stream)), fn.__name__, temp, stream)
 
     def ArgMin(self, temp_storage, d_in, d_out, d_index_out, num_item: int, stream=None):
         """device_reduce.h:187-227: smallest value, ties to the smallest index."""
@@ -134,10 +153,10 @@ class DeviceReduce:
         code = dtype_code(d_in.dtype)
         np_dt = [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64][code]
         iv = np.array([init], dtype=np_dt)
-        check(lib().lcpp_reduce_transform(code, LCPP_OPS[reduce_op], LCPP_TRANSFORMS[transform_op], _ptr(temp_storage),
+        self._check(lib().lcpp_reduce_transform(code, LCPP_OPS[reduce_op], LCPP_TRANSFORMS[transform_op], _ptr(temp_storage),
                                           _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), num_item,
                                           ctypes.c_void_p(iv.ctypes.data), _stream(stream)),
-              "lcpp_reduce_transform")
+              "lcpp_reduce_transform", temp_storage, stream)
 
     @staticmethod
     def GetReduceByKeyTempStorageBytes(key_dtype, value_dtype, num_elements: int) -> int:
@@ -159,21 +178,16 @@ class DeviceReduce:
             raise TypeError("ReduceByKey: g_num_runs_out must hold a 32-bit count")
         if reduce_op not in LCPP_OPS:
             raise ValueError(f"ReduceByKey: unsupported reduce_op {reduce_op!r}")
-        check(lib().lcpp_reduce_by_key(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype), LCPP_OPS[reduce_op],
+        self._check(lib().lcpp_reduce_by_key(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype), LCPP_OPS[reduce_op],
                                        _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_keys_in), _ptr(d_values_in),
                                        _ptr(d_unique_out), _ptr(g_aggregates_out), _ptr(g_num_runs_out), num_elements,
                                        _stream(stream)),
-              "lcpp_reduce_by_key")
+              "lcpp_reduce_by_key", temp_storage, stream)
 
 
-class DeviceScan:
+class DeviceScan(_Module):
     """device/device_scan.h:33-339 (ExclusiveSum / InclusiveSum / *ScanByKey / *SumByKey)."""
 
-    def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
-        self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
-
-    def create(self, device=None, debug_stream=None):
-        return self
 
     @staticmethod
     def GetTempStorageBytes(dtype, num_items: int) -> int:
@@ -183,8 +197,8 @@ class DeviceScan:
         _need(d_in, num_items, "d_in")
         _need(d_out, num_items, "d_out")
         _same_dtype(d_in, d_out, fn.__name__)
-        check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), num_items,
-                 _stream(stream)), fn.__name__)
+        self._check(fn(dtype_code(d_in.dtype), _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), num_items,
+                 _stream(stream)), fn.__name__, temp, stream)
 
     def ExclusiveSum(self, temp_storage, d_in, d_out, num_items: int, stream=None):
         self._run(lib().lcpp_scan_exclusive_sum, temp_storage, d_in, d_out, num_items, stream)
@@ -206,9 +220,9 @@ class DeviceScan:
             raise ValueError(f"{name}: unsupported scan_op {op!r}")
         vcode = dtype_code(d_values_in.dtype)
         iv = _host_value(vcode, init)
-        check(fn(dtype_code(d_keys_in.dtype), vcode, LCPP_OPS[op], _ptr(temp), _nbytes(temp), _ptr(d_keys_in),
+        self._check(fn(dtype_code(d_keys_in.dtype), vcode, LCPP_OPS[op], _ptr(temp), _nbytes(temp), _ptr(d_keys_in),
                  _ptr(d_values_in), _ptr(d_values_out), num_items, ctypes.c_void_p(iv.ctypes.data), _stream(stream)),
-              name)
+              name, temp, stream)
 
     def ExclusiveScanByKey(self, temp_storage, d_keys_in, d_values_in, d_values_out, scan_op: str, num_items: int,
                            initial_value, stream=None):
@@ -232,14 +246,9 @@ class DeviceScan:
         self.InclusiveScanByKey(temp_storage, d_keys_in, d_values_in, d_values_out, "sum", num_items, 0, stream)
 
 
-class DeviceRadixSort:
+class DeviceRadixSort(_Module):
     """device/device_radix_sort.h:37-184 (onesweep SortKeys / SortPairs, ascending and descending)."""
 
-    def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
-        self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
-
-    def create(self, device=None, debug_stream=None):
-        return self
 
     @staticmethod
     def GetSortKeysTempStorageBytes(key_dtype, num_items: int) -> int:
@@ -254,8 +263,8 @@ class DeviceRadixSort:
         _need(d_keys_in, num_items, "d_keys_in")
         _need(d_keys_out, num_items, "d_keys_out")
         _same_dtype(d_keys_in, d_keys_out, name)
-        check(fn(dtype_code(d_keys_in.dtype), _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_keys_in),
-                 _ptr(d_keys_out), num_items, _stream(stream)), name)
+        self._check(fn(dtype_code(d_keys_in.dtype), _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_keys_in),
+                 _ptr(d_keys_out), num_items, _stream(stream)), name, temp_storage, stream)
 
     def _pairs(self, fn, name, temp_storage, d_keys_in, d_keys_out, d_values_in, d_values_out, num_items, stream):
         for t, nm in ((d_keys_in, "d_keys_in"), (d_keys_out, "d_keys_out"), (d_values_in, "d_values_in"),
@@ -263,9 +272,9 @@ class DeviceRadixSort:
             _need(t, num_items, nm)
         _same_dtype(d_keys_in, d_keys_out, name + " keys")
         _same_dtype(d_values_in, d_values_out, name + " values")
-        check(fn(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype), _ptr(temp_storage),
+        self._check(fn(dtype_code(d_keys_in.dtype), dtype_code(d_values_in.dtype), _ptr(temp_storage),
                  _nbytes(temp_storage), _ptr(d_keys_in), _ptr(d_keys_out), _ptr(d_values_in), _ptr(d_values_out),
-                 num_items, _stream(stream)), name)
+                 num_items, _stream(stream)), name, temp_storage, stream)
 
     def SortKeys(self, temp_storage, d_keys_in, d_keys_out, num_items: int, stream=None):
         self._keys(lib().lcpp_radix_sort_keys, "lcpp_radix_sort_keys", temp_storage, d_keys_in, d_keys_out,
@@ -288,16 +297,11 @@ class DeviceRadixSort:
                     d_keys_in, d_keys_out, d_values_in, d_values_out, num_items, stream)
 
 
-class DeviceSegmentReduce:
+class DeviceSegmentReduce(_Module):
     """device/device_segment_reduce.h:26-349: Reduce / Sum / Min / Max / ArgMin / ArgMax over CSR
     begin/end offsets or over fixed-size segments (pass segment_size, an int, in place of the two
     offset buffers, as the reference's overloads do)."""
 
-    def __init__(self, BLOCK_SIZE: int = 256, WARP_NUMS: int = 64, ITEMS_PER_THREAD: int = 16):
-        self.geometry = (BLOCK_SIZE, WARP_NUMS, ITEMS_PER_THREAD)
-
-    def create(self, device=None, debug_stream=None):
-        return self
 
     @staticmethod
     def GetTempStorageBytes(dtype, num_item: int = 0) -> int:
@@ -308,10 +312,17 @@ class DeviceSegmentReduce:
         """device_segment_reduce.h:77-89 (0 here: no key-value staging)"""
         return _query(lib().lcpp_segment_reduce_arg_temp_bytes, dtype_code(dtype), num_item, num_segments)
 
-    @staticmethod
-    def _check_ranges(d_in, num_segments, offsets):
-        """Every segment must lie inside d_in (checked on the host: bad offsets
-        raise instead of faulting the GPU)."""
+    # The library reads every segment the offsets name, as the reference does
+    # (device_segment_reduce.h:353-381 validates nothing).  With
+    # validate_offsets = True (or a debug stream) the CSR offsets are checked
+    # against d_in on the host first, which synchronizes on a device-to-host
+    # read; by default no call synchronizes.  Fixed-size segments are always
+    # checked (host arithmetic only).
+    validate_offsets = False
+
+    def _check_ranges(self, d_in, num_segments, offsets):
+        """Every segment must lie inside d_in: bad offsets raise instead of
+        faulting the GPU."""
         if not num_segments:
             return
         if isinstance(offsets[0], int):
@@ -326,6 +337,8 @@ class DeviceSegmentReduce:
         d_begin_offsets, d_end_offsets = offsets
         _need(d_begin_offsets, num_segments, "d_begin_offsets")
         _need(d_end_offsets, num_segments, "d_end_offsets")
+        if not (self.validate_offsets or self._debug):
+            return
         b = d_begin_offsets[:num_segments].to(torch.int64)
         e = d_end_offsets[:num_segments].to(torch.int64)
         hi = torch.where(e > b, e, torch.zeros_like(e)).max().item()
@@ -343,14 +356,14 @@ class DeviceSegmentReduce:
         ip = ctypes.c_void_p(iv.ctypes.data) if iv is not None else ctypes.c_void_p(0)
         L = lib()
         if isinstance(offsets[0], int):
-            check(L.lcpp_segment_reduce_fixed(code, LCPP_OPS[op], _ptr(temp_storage), _nbytes(temp_storage),
+            self._check(L.lcpp_segment_reduce_fixed(code, LCPP_OPS[op], _ptr(temp_storage), _nbytes(temp_storage),
                                               _ptr(d_in), _ptr(d_out), num_segments, offsets[0], ip, _stream(stream)),
-                  "lcpp_segment_reduce_fixed")
+                  "lcpp_segment_reduce_fixed", None, stream)
         else:
-            check(L.lcpp_segment_reduce(code, LCPP_OPS[op], _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in),
+            self._check(L.lcpp_segment_reduce(code, LCPP_OPS[op], _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in),
                                         _ptr(d_out), num_segments, _ptr(offsets[0]), _ptr(offsets[1]), ip,
                                         _stream(stream)),
-                  "lcpp_segment_reduce")
+                  "lcpp_segment_reduce", None, stream)
 
     def Reduce(self, temp_storage, d_in, d_out, num_segments: int, *args, stream=None):
         """Reduce(temp, d_in, d_out, num_segments, d_begin_offsets, d_end_offsets, reduce_op, initial_value)
@@ -394,12 +407,12 @@ class DeviceSegmentReduce:
         code = dtype_code(d_in.dtype)
         if isinstance(offsets[0], int):
             fn = L.lcpp_segment_reduce_argmax_fixed if is_max else L.lcpp_segment_reduce_argmin_fixed
-            check(fn(code, _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
-                     num_segments, offsets[0], _stream(stream)), fn.__name__)
+            self._check(fn(code, _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
+                     num_segments, offsets[0], _stream(stream)), fn.__name__, None, stream)
         else:
             fn = L.lcpp_segment_reduce_argmax if is_max else L.lcpp_segment_reduce_argmin
-            check(fn(code, _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
-                     num_segments, _ptr(offsets[0]), _ptr(offsets[1]), _stream(stream)), fn.__name__)
+            self._check(fn(code, _ptr(temp_storage), _nbytes(temp_storage), _ptr(d_in), _ptr(d_out), _ptr(d_index_out),
+                     num_segments, _ptr(offsets[0]), _ptr(offsets[1]), _stream(stream)), fn.__name__, None, stream)
 
     def ArgMax(self, temp_storage, d_in, d_out, d_index_out, num_segments: int, *offsets, stream=None):
         """device_segment_reduce.h:197-272: the largest value and its index within the segment

@@ -9,6 +9,10 @@
 // BufferView, a CommandList holding a hipStream_t).  Prints one line per case
 // and exits non-zero on the first mismatch.  Built by __graft_entry__.build()
 // (g++, links liblcpp_amd.so); run by tests/test_gpu_cpp_api.py.
+//
+// Built as a release build (NDEBUG): check() records a failed call's status
+// instead of aborting, so the debug-stream case below can read last_status().
+#define NDEBUG
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
@@ -275,6 +279,50 @@ void test_segment_reduce()
     expect(ok, "DeviceSegmentReduce::ArgMin fixed 32");
 }
 
+// create(device, &stream), as the reference's modules take a debug stream:
+// every call is synchronized and its device status word read, so a
+// look-back wait that gave up is reported by the call that caused it.  The
+// give-up is forced with the test hook (a tile that never publishes; every
+// kernel still drains).
+void test_debug_stream()
+{
+    Device device{0};
+    Stream debug{g_stream};
+    CommandList cmdlist{g_stream};
+    DeviceScan<> scanner;
+    scanner.create(device, &debug);
+    const size_t n = size_t(1) << 20;
+    DevBuf<uint> in(std::vector<uint>(n, 1u)), out(n);
+    Temp temp(DeviceScan<>::GetTempStorageBytes<uint>(n));
+    scanner.ExclusiveSum(cmdlist, temp.view(), in.view(), out.view(), n);
+    expect(scanner.last_status() == LCPP_OK, "debug stream: DeviceScan::ExclusiveSum status");
+    lcpp_test_set_lookback_fault(3, 32);
+    scanner.ExclusiveSum(cmdlist, temp.view(), in.view(), out.view(), n);
+    lcpp_test_set_lookback_fault(0xFFFFFFFFu, 0);
+    expect(scanner.last_status() == LCPP_ERR_LOOKBACK_TIMEOUT, "debug stream: withheld scan tile reported");
+    scanner.ExclusiveSum(cmdlist, temp.view(), in.view(), out.view(), n);
+    const std::vector<uint> h = out.download(n);
+    bool ok = scanner.last_status() == LCPP_OK;
+    for (size_t i = 0; i < n && ok; ++i) ok = h[i] == i;
+    expect(ok, "debug stream: DeviceScan::ExclusiveSum after the fault");
+
+    DeviceRadixSort<> sorter;
+    sorter.create(device, &debug);
+    const uint m = 1u << 20;
+    std::vector<uint> keys(m);
+    for (uint i = 0; i < m; ++i) keys[i] = (i * 2654435761u) ^ 0x5bd1e995u;
+    DevBuf<uint> kin(keys), kout(m);
+    Temp t2(DeviceRadixSort<>::GetSortKeysTempStorageBytes<uint>(m));
+    lcpp_test_set_lookback_fault(9, 32);
+    sorter.SortKeys(cmdlist, t2.view(), kin.view(), kout.view(), m);
+    lcpp_test_set_lookback_fault(0xFFFFFFFFu, 0);
+    expect(sorter.last_status() == LCPP_ERR_LOOKBACK_TIMEOUT, "debug stream: withheld sort tile reported");
+    sorter.SortKeys(cmdlist, t2.view(), kin.view(), kout.view(), m);
+    std::vector<uint> hk = kout.download(m);
+    std::sort(keys.begin(), keys.end());
+    expect(sorter.last_status() == LCPP_OK && hk == keys, "debug stream: DeviceRadixSort::SortKeys after the fault");
+}
+
 }  // namespace
 
 int main()
@@ -284,6 +332,7 @@ int main()
     test_scan();
     test_sort();
     test_segment_reduce();
+    test_debug_stream();
     hip_ok(hipStreamDestroy(g_stream), "hipStreamDestroy");
     std::printf("%s: %d failure(s)\n", g_failures ? "FAILED" : "PASSED", g_failures);
     return g_failures ? 1 : 0;

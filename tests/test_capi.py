@@ -56,48 +56,58 @@ def _q(fn, *args):
     return rc, out.value
 
 
+# every temp layout starts with the 256-byte status header (lcpp_temp_status)
+HDR = 256
+
+
 def test_temp_bytes_queries(L):
     # reduce: one partial per workgroup (<= 512; <= 1024 for arg), none when one workgroup suffices
     assert _q(L.lcpp_reduce_temp_bytes, 0, 0) == (0, 0)
     assert _q(L.lcpp_reduce_temp_bytes, 0, 8192) == (0, 0)
     rc, b = _q(L.lcpp_reduce_temp_bytes, 0, 1 << 28)  # one partial per workgroup, at most 512
-    assert rc == 0 and b == 512 * 4
+    assert rc == 0 and b == HDR + 512 * 4
     rc, b = _q(L.lcpp_reduce_temp_bytes, 5, 1 << 28)
-    assert rc == 0 and b == 512 * 8
+    assert rc == 0 and b == HDR + 512 * 8
     assert _q(L.lcpp_reduce_temp_bytes, 0, 32768) == (0, 0)  # one 128 KiB tile: one workgroup, no temp
-    assert _q(L.lcpp_reduce_temp_bytes, 0, 32769) == (0, 256)
+    assert _q(L.lcpp_reduce_temp_bytes, 0, 32769) == (0, HDR + 256)
     # arg reduce: one (value, index) partial per workgroup
     rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 2, 1 << 28)
-    assert rc == 0 and b == 1024 * 8
+    assert rc == 0 and b == HDR + 1024 * 8
     rc, b = _q(L.lcpp_reduce_arg_temp_bytes, 5, 1 << 28)
-    assert rc == 0 and b == 1024 * 16
+    assert rc == 0 and b == HDR + 1024 * 16
     assert _q(L.lcpp_reduce_arg_temp_bytes, 0, 100) == (0, 0)
     # scan: one packed 64-bit word per tile (two for 64-bit types), counted for
     # the smaller of the exclusive (20480 / 10240) and inclusive (16384 / 8192;
     # 24576 for float) integer tiles
     rc, b = _q(L.lcpp_scan_temp_bytes, 1, 1 << 28)
-    assert rc == 0 and b == (1 << 14) * 8
+    assert rc == 0 and b == HDR + (1 << 14) * 8
     rc, b = _q(L.lcpp_scan_temp_bytes, 4, 1 << 27)
-    assert rc == 0 and b == (1 << 14) * 16
-    # sort: bins + hot digits + 2 regions of tile counts + 2 regions of batch words (8 bytes
-    # each; keys-only passes use 4) + key scratch (no value scratch for keys-only);
-    # 16384-key tiles, batches of 8
+    assert rc == 0 and b == HDR + (1 << 14) * 16
+    assert _q(L.lcpp_scan_temp_bytes, 1, 0) == (0, 0)
+    # sort: header + bins + hot digits + plan + arrival counter, then 2 regions of
+    # tile counts + 2 regions of 64-bit batch words + key scratch (no value
+    # scratch for keys-only); 16384-key tiles (8192 with values), batches of 8
     rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, 1 << 28)
     tiles = (1 << 28) // 16384
-    bins_and_hot = (4 * 256 * 4 + 4 * 4 + 255) // 256 * 256  # digit bins + one hot digit per pass
-    assert rc == 0 and b == bins_and_hot + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 8 + (1 << 28) * 4
+    head = (HDR + 4 * 256 * 4 + (2 * 4 + 1) * 4 + 255) // 256 * 256
+    assert rc == 0 and b == head + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 8 + (1 << 28) * 4
     rc, bp = _q(L.lcpp_radix_sort_pairs_temp_bytes, 4, 1, 1 << 27)
-    assert rc == 0 and bp > (1 << 27) * 12
+    tiles = (1 << 27) // 8192
+    head = (HDR + 8 * 256 * 4 + (2 * 8 + 1) * 4 + 255) // 256 * 256
+    assert rc == 0 and bp == head + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 8 + (1 << 27) * 12
+    # the sort takes n up to 2^32 - 1 (32-bit look-back counts and positions)
+    rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, (1 << 32) - 1)
+    assert rc == 0 and b > ((1 << 32) - 1) * 4
     # scan by key: one packed word per 8192-value tile (two for 8-byte values)
     rc, b = _q(L.lcpp_scan_by_key_temp_bytes, 0, 2, 1 << 28)
-    assert rc == 0 and b == (1 << 15) * 8
+    assert rc == 0 and b == HDR + (1 << 15) * 8
     rc, b = _q(L.lcpp_scan_by_key_temp_bytes, 2, 5, 1 << 27)
-    assert rc == 0 and b == (1 << 15) * 16
+    assert rc == 0 and b == HDR + (1 << 15) * 16
     # reduce by key: head-count words + open-run words, each 256-byte aligned
     rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 0, 0, 1 << 28)
-    assert rc == 0 and b == 2 * (1 << 15) * 8
+    assert rc == 0 and b == HDR + 2 * (1 << 15) * 8
     rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 5, 5, 100)
-    assert rc == 0 and b == 256 + 256
+    assert rc == 0 and b == HDR + 256 + 256
     assert _q(L.lcpp_reduce_by_key_temp_bytes, 0, 9, 100)[0] == -3
     # segment reduce needs none (as the reference)
     assert _q(L.lcpp_segment_reduce_temp_bytes, 2, 1 << 20) == (0, 0)
@@ -117,7 +127,9 @@ def test_unsupported_dtype_and_null_args(L):
     assert L.lcpp_reduce_transform(0, 0, 9, None, 0, None, None, 10, ctypes.byref(one), None) == -1  # bad transform
     assert L.lcpp_scan_exclusive_sum(0, None, 0, None, None, 10, None) == -1
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 10, None) == -1
-    assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 1 << 30, None) == -1  # n >= 2^30
+    assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 1 << 30, None) == -1  # no temp
+    dummy = ctypes.c_void_p(0x1000)
+    assert L.lcpp_radix_sort_keys(1, dummy, 1 << 40, dummy, dummy, 1 << 32, None) == -1  # n >= 2^32
     assert L.lcpp_radix_sort_keys_descending(1, None, 0, None, None, 10, None) == -1
     assert L.lcpp_radix_sort_pairs_descending(1, 9, None, 0, None, None, None, None, 10, None) == -3
     assert L.lcpp_radix_sort_pairs_descending(4, 1, None, 0, None, None, None, None, 10, None) == -1
@@ -151,6 +163,16 @@ def test_temp_too_small_detected_before_launch(L):
     assert L.lcpp_scan_inclusive_sum_by_key(0, 0, dummy, 16, dummy, dummy, dummy, 1 << 20, None) == -2
     assert L.lcpp_reduce_by_key(0, 0, 0, dummy, 16, dummy, dummy, dummy, dummy, dummy, 1 << 20, None) == -2
     assert L.lcpp_reduce_by_key(0, 0, 0, dummy, 1 << 30, dummy, dummy, dummy, dummy, dummy, 1 << 32, None) == -1
+
+
+def test_device_status_decode_and_hooks(L):
+    # the status word's bits map to status codes without a GPU
+    assert L.lcpp_device_status_decode(0) == 0
+    assert L.lcpp_device_status_decode(1) == -5
+    assert L.lcpp_device_status_decode(0x80000001) == -5
+    assert L.lcpp_status_string(-5) == b"LCPP_ERR_LOOKBACK_TIMEOUT"
+    assert L.lcpp_test_set_lookback_fault(3, 16) == 0
+    assert L.lcpp_test_set_lookback_fault(0xFFFFFFFF, 0) == 0  # back to the defaults
 
 
 def test_misaligned_temp_rejected(L):

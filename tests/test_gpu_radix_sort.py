@@ -126,7 +126,7 @@ def test_pairs_stable_vs_oracle(gpu, kdt, vdt, n):
 def test_lookback_batch_boundaries(gpu, kdt, vdt, tiles, delta):
     import gpu_util as g
 
-    tile = 8192 if np.dtype(kdt).itemsize == 8 or (vdt is not None and np.dtype(vdt).itemsize == 8) else 16384
+    tile = 8192 if np.dtype(kdt).itemsize == 8 or vdt is not None else 16384
     n = tiles * tile + delta
     k = g.random_array(kdt, n, seed=tiles * 7 + delta)
     log(f"sort batch boundaries {np.dtype(kdt).name}/{vdt and np.dtype(vdt).name} n={n}")
@@ -286,3 +286,103 @@ def test_trivial_passes_skipped(gpu, kdt, mask, descending):
     ko, vo = sort_pairs(g.to_dev(k), g.to_dev(v), n, kdt, np.uint32, descending=descending)
     rk, rv = o.radix_sort(k, v, descending=descending)
     assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
+
+
+# ---------------------------------------------------------------- LDS lane order
+@pytest.mark.parametrize("pattern", [0, 1, 2, 3])
+def test_lds_atomic_lane_order_probe(gpu, pattern):
+    """The stable ranking relies on gfx950 returning same-address LDS atomic
+    adds of one instruction in lane order (not an ISA guarantee): a probe over
+    uniform, skewed, constant and two-valued digits, 2^24 lane operations
+    each, must find no exception."""
+    from lc_parallel_primitive_amd import datagen
+
+    log(f"LDS lane-order probe pattern={pattern}")
+    assert datagen.lds_order_probe(0x51AB + pattern, pattern, waves=4096, rounds=64) == 0
+
+
+# ---------------------------------------------------------------- device checkers, pinned
+def _mix64(x):
+    z = x.astype(np.uint64)
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def _host_hash(a):
+    with np.errstate(over="ignore"):
+        return (int(np.count_nonzero(a[:-1] > a[1:])), int(a.astype(np.uint64).sum(dtype=np.uint64)),
+                int(_mix64(a).sum(dtype=np.uint64)))
+
+
+def test_device_checkers_match_oracle(gpu):
+    """The device-side checkers used at sizes above 2^30 agree with the host
+    (oracle) checkers, and catch planted mistakes: an adjacent swap, a changed
+    key, equal keys whose values are swapped, a value out of range."""
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 100_003
+    k = g.random_array(np.uint32, n, seed=77) & np.uint32(0xFFF)
+    v = np.arange(n, dtype=np.uint32)
+    sk, sv = o.radix_sort(k, v)
+    assert datagen.sorted_hash_u32(g.to_dev(k))[1:] == datagen.sorted_hash_u32(g.to_dev(sk))[1:]
+    assert datagen.sorted_hash_u32(g.to_dev(sk)) == _host_hash(sk)
+    assert datagen.sorted_hash_u32(g.to_dev(sk))[0] == 0
+    assert datagen.check_stable_pairs_u32(g.to_dev(k), g.to_dev(sk), g.to_dev(sv)) == 0
+    assert o.check_stable_pairs_u64_u32(k.astype(np.uint64), sk.astype(np.uint64), sv)
+    i = int(np.flatnonzero(sk[1:] != sk[:-1])[10])  # sk[i] < sk[i+1]
+    bad = sk.copy()
+    bad[i], bad[i + 1] = bad[i + 1], bad[i]
+    assert datagen.sorted_hash_u32(g.to_dev(bad))[0] == 1
+    bad = sk.copy()
+    bad[5] ^= 1
+    assert datagen.sorted_hash_u32(g.to_dev(bad))[1:] != datagen.sorted_hash_u32(g.to_dev(sk))[1:]
+    j = int(np.flatnonzero(sk[1:] == sk[:-1])[3])  # equal keys at j, j+1
+    bv = sv.copy()
+    bv[j], bv[j + 1] = bv[j + 1], bv[j]
+    assert datagen.check_stable_pairs_u32(g.to_dev(k), g.to_dev(sk), g.to_dev(bv)) > 0
+    assert not o.check_stable_pairs_u64_u32(k.astype(np.uint64), sk.astype(np.uint64), bv)
+    bv = sv.copy()
+    bv[7] = n
+    assert datagen.check_stable_pairs_u32(g.to_dev(k), g.to_dev(sk), g.to_dev(bv)) > 0
+
+
+# ---------------------------------------------------------------- n >= 2^30
+def test_keys_above_2p30(gpu):
+    """n = 2^30 + 12345 uint32 keys (the output spans more than 2^32 bytes, so
+    the 64-bit write-out path runs): sorted, and the same multiset as the
+    input (order-independent sums of the keys and of mix64 of the keys)."""
+    import torch
+
+    from lc_parallel_primitive_amd import datagen
+
+    n = (1 << 30) + 12345
+    log(f"sort keys u32 n={n}")
+    d = datagen.keys_u32(n, seed=0x2B30)
+    h_in = datagen.sorted_hash_u32(d)
+    out = sort_keys(d, n, np.uint32)
+    torch.cuda.synchronize()
+    h_out = datagen.sorted_hash_u32(out)
+    assert h_out[0] == 0 and h_out[1:] == h_in[1:]
+    del d, out
+
+
+def test_pairs_stable_above_2p30(gpu):
+    """n = 2^30 + 777 uint32 keys with 16 random bits (heavy duplication) and
+    values = index: the device O(N) stability checker finds no bad position."""
+    import torch
+
+    from lc_parallel_primitive_amd import datagen
+
+    n = (1 << 30) + 777
+    log(f"sort pairs u32/u32 n={n}")
+    k = datagen.keys_u32(n, seed=0x2B31)
+    k.view(torch.int32).bitwise_and_(0xFFFF)
+    v = datagen.iota_u32(n)
+    ko, vo = sort_pairs(k, v, n, np.uint32, np.uint32)
+    torch.cuda.synchronize()
+    del v
+    assert datagen.check_stable_pairs_u32(k, ko, vo) == 0
+    del k, ko, vo
