@@ -66,8 +66,10 @@ typedef enum lcpp_status {
     LCPP_ERR_TEMP_TOO_SMALL = -2,   /* temp_bytes < the *_temp_bytes query result */
     LCPP_ERR_UNSUPPORTED_DTYPE = -3,
     LCPP_ERR_HIP = -4,              /* a HIP runtime call or kernel launch failed */
-    LCPP_ERR_LOOKBACK_TIMEOUT = -5  /* reported by lcpp_temp_status: a look-back wait gave up,
+    LCPP_ERR_LOOKBACK_TIMEOUT = -5, /* reported by lcpp_temp_status: a look-back wait gave up,
                                        so that call's output is wrong */
+    LCPP_ERR_SIZE_LIMIT = -6        /* n exceeds what lcpp_scan_exclusive_sum_noalloc's fixed
+                                       scratch covers */
 } lcpp_status;
 
 /* Bits of the device status word kept in the first 4 bytes of temp storage. */
@@ -154,6 +156,15 @@ int lcpp_scan_exclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const v
 /* replaces DeviceScan::InclusiveSum, device_scan.h:193-204: out[i] = sum(in[0..i]) */
 int lcpp_scan_inclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in,
                             void *out, uint64_t n, void *stream);
+/* No counterpart in the reference.  For callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * same result as lcpp_scan_exclusive_sum with no temp argument and no allocation.
+ * Its look-back state lives in a fixed 512 KiB device array inside the library,
+ * one per GPU, so n <= 1,342,177,280 for 4-byte types and n <= 335,544,320 for
+ * 8-byte types (larger n: LCPP_ERR_SIZE_LIMIT).  Every call on a GPU shares that
+ * GPU's array: calls that overlap in time on one GPU race (serialize them, e.g.
+ * on one stream).  A look-back give-up is not reported (no temp to query). */
+int lcpp_scan_exclusive_sum_noalloc(lcpp_dtype t, const void *in, void *out, uint64_t n, void *stream);
 
 /* ---------------------------------------------------------------------
  * ScanByKey / ReduceByKey — device/device_scan.h, device/device_reduce.h

@@ -91,6 +91,7 @@ extern "C" const char *lcpp_status_string(int status)
     case LCPP_ERR_UNSUPPORTED_DTYPE: return "LCPP_ERR_UNSUPPORTED_DTYPE";
     case LCPP_ERR_HIP: return "LCPP_ERR_HIP";
     case LCPP_ERR_LOOKBACK_TIMEOUT: return "LCPP_ERR_LOOKBACK_TIMEOUT";
+    case LCPP_ERR_SIZE_LIMIT: return "LCPP_ERR_SIZE_LIMIT";
     default: return "LCPP_ERR_UNKNOWN";
     }
 }

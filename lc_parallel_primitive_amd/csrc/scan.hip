@@ -179,6 +179,38 @@ void scan_kernel(const T *__restrict__ in,
     }
 }
 
+// Enqueue one scan whose status header + look-back words start at `head`
+// (zeroed here by a fill kernel, so the call can be graph-captured).
+// `instrument`: bracket the launches with the profiling events when enabled.
+template <class T>
+int scan_run(bool inclusive, uint64_t *head, const T *in, T *out, uint64_t n, uint64_t tiles, hipStream_t s,
+             bool instrument)
+{
+    uint64_t *words = head + kStatusBytes / 8;
+    const uint64_t nwords = kStatusBytes / 8 + tiles * (sizeof(T) == 4 ? 1 : 2);
+    const WaitCtl ctl = wait_ctl(reinterpret_cast<uint32_t *>(head));
+    const int vec_ok = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (instrument) {
+        if (lb_init(head, nwords, s, "scan_init") != LCPP_OK) return LCPP_ERR_HIP;
+        if (inclusive)
+            LCPP_LAUNCH("scan_inclusive", s,
+                        scan_kernel<T, true><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
+        else
+            LCPP_LAUNCH("scan_exclusive", s,
+                        scan_kernel<T, false><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
+    } else {
+        const uint64_t g = ceil_div(nwords, 256);
+        lb_init_kernel<<<(uint32_t)(g < 1024 ? g : 1024), 256, 0, s>>>(head, nwords);
+        if (hipGetLastError() != hipSuccess) return LCPP_ERR_HIP;
+        if (inclusive)
+            scan_kernel<T, true><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl);
+        else
+            scan_kernel<T, false><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl);
+    }
+    LCPP_CHECK_LAUNCH();
+    return LCPP_OK;
+}
+
 template <class T>
 int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, void *out_,
                 uint64_t n, hipStream_t s)
@@ -191,20 +223,7 @@ int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, 
     if (tiles > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;
     if (temp_bytes < scan_temp_bytes<T>(n)) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
-    uint64_t *head = static_cast<uint64_t *>(temp);  // status header, then the look-back words
-    uint64_t *words = head + kStatusBytes / 8;
-    const uint64_t nwords = tiles * (sizeof(T) == 4 ? 1 : 2);
-    if (lb_init(head, kStatusBytes / 8 + nwords, s, "scan_init") != LCPP_OK) return LCPP_ERR_HIP;
-    const WaitCtl ctl = wait_ctl(static_cast<uint32_t *>(temp));
-    const int vec_ok = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-    if (inclusive)
-        LCPP_LAUNCH("scan_inclusive", s,
-                    scan_kernel<T, true><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
-    else
-        LCPP_LAUNCH("scan_exclusive", s,
-                    scan_kernel<T, false><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
-    LCPP_CHECK_LAUNCH();
-    return LCPP_OK;
+    return scan_run<T>(inclusive, static_cast<uint64_t *>(temp), in, out, n, tiles, s, true);
 }
 
 int scan_dispatch(bool inclusive, lcpp_dtype t, void *temp, size_t tb, const void *in, void *out,
@@ -247,4 +266,64 @@ extern "C" int lcpp_scan_inclusive_sum(lcpp_dtype t, void *temp, size_t tb, cons
                                        void *out, uint64_t n, void *stream)
 {
     return scan_dispatch(true, t, temp, tb, in, out, n, stream);
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// lcpp_scan_exclusive_sum_noalloc: the status header and look-back words live
+// in `scratch`, a file-scope device array (each GPU the library runs on holds
+// its own copy until the process ends), so the call allocates nothing.  Host
+// code never uses the array's name as an address: its device address is
+// fetched once per device with hipGetSymbolAddress and kept per device.
+// Calls that overlap on one GPU share the array and race.
+namespace {
+constexpr uint64_t kNoAllocWords = kStatusBytes / 8 + 65536;  // 512 KiB of look-back words
+}  // namespace
+static __device__ __align__(256) uint64_t scratch[kNoAllocWords];
+
+namespace {
+std::atomic<uint64_t *> g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch` (looked up on its first use).
+int scratch_ptr(uint64_t **out)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LCPP_ERR_HIP;
+    uint64_t *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        void *q = nullptr;
+        if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return LCPP_ERR_HIP;
+        p = static_cast<uint64_t *>(q);
+        g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return LCPP_OK;
+}
+
+template <class T>
+int scan_noalloc(const void *in_, void *out_, uint64_t n, hipStream_t s)
+{
+    if (n == 0) return LCPP_OK;
+    const T *in = static_cast<const T *>(in_);
+    T *out = static_cast<T *>(out_);
+    if (!in || !out) return LCPP_ERR_INVALID_ARG;
+    const uint64_t tiles = scan_tiles<T, false>(n);
+    if (kStatusBytes / 8 + tiles * (sizeof(T) == 4 ? 1 : 2) > kNoAllocWords) return LCPP_ERR_SIZE_LIMIT;
+    uint64_t *head = nullptr;
+    if (scratch_ptr(&head) != LCPP_OK) return LCPP_ERR_HIP;
+    return scan_run<T>(false, head, in, out, n, tiles, s, false);
+}
+}  // namespace
+
+extern "C" int lcpp_scan_exclusive_sum_noalloc(lcpp_dtype t, const void *in, void *out, uint64_t n, void *stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (t) {
+    case LCPP_INT32: return scan_noalloc<int32_t>(in, out, n, s);
+    case LCPP_UINT32: return scan_noalloc<uint32_t>(in, out, n, s);
+    case LCPP_FLOAT32: return scan_noalloc<float>(in, out, n, s);
+    case LCPP_INT64: return scan_noalloc<int64_t>(in, out, n, s);
+    case LCPP_UINT64: return scan_noalloc<uint64_t>(in, out, n, s);
+    case LCPP_FLOAT64: return scan_noalloc<double>(in, out, n, s);
+    default: return LCPP_ERR_UNSUPPORTED_DTYPE;
+    }
 }
