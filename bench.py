@@ -8,9 +8,14 @@ keys uniform over the full 32-bit range (histogram + 4 onesweep passes),
 keys resident in HBM.  One step = one SortKeys call through the C ABI.
 Prints ONE JSON line.  `roofline` is the dominant kernel (the onesweep pass)
 measured live with HIP events recorded by the library on the launch stream;
-`secondary` holds the scan / reduce / pairs / low-entropy / segment-reduce
-configurations; `cpu_baseline` times the CPU onesweep restatement (oracle/)
-on a bounded sample on this host.
+`secondary` holds every other BASELINE configuration (reduce 2^24 with the
+256 MB MALL flushed before each timed call and unflushed beside it, reduce
+2^28, both scans, the low-entropy sort, SortPairs as configured and with all
+8 digit passes moving data, the by-key primitives, segment reduce), each with
+its dominant kernel's time and, where BASELINE names one, a CPU number;
+`cpu_baseline` and those per-entry CPU numbers time the oracle's C
+restatements of the reference algorithms (oracle/) on bounded samples on
+this host's cores.
 """
 from __future__ import annotations
 
@@ -179,16 +184,42 @@ def main():
     # ------------------------------------------------------------ secondary configurations
     if not args.no_secondary:
         sec = []
+        flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")  # > the 256 MB MALL
 
-        def add(name, unit_bytes, call, steps, kname, items=None, unit="GB/s"):
-            t = timed(call, steps, 2)
+        def flushed_ms(call, reps):
+            """Median device time of one call with the MALL flushed before it (a 1 GiB write
+            between calls, outside the timed events)."""
+            for _ in range(2):
+                call()
+            ts = []
+            for r in range(reps):
+                flush_buf.fill_(r & 0xFF)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                call()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            return statistics.median(ts)
+
+        def add(name, unit_bytes, call, steps, kname, items=None, cpu=None, flushed=False, note=None):
+            t = flushed_ms(call, steps) if flushed else timed(call, steps, 2)
             kms, _, _ = kernel_ms(call, max(2, steps // 2), kname)
             gbs = unit_bytes / (t * 1e-3) / 1e9
             entry = {"workload": name, "ms": round(t, 4), "GB/s": round(gbs, 1),
                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                      "dominant_kernel": kname, "kernel_us": round(kms * 1e3, 2)}
+            if flushed:
+                tu = timed(call, steps, 2)
+                entry["mall"] = "flushed (1 GiB written before each timed call)"
+                entry["unflushed_ms"] = round(tu, 4)
+                entry["unflushed_GB/s"] = round(unit_bytes / (tu * 1e-3) / 1e9, 1)
             if items is not None:
                 entry["Gitems/s"] = round(items / (t * 1e-3) / 1e9, 3)
+            if note:
+                entry["note"] = note
+            if cpu is not None and not args.no_cpu_baseline:
+                entry["cpu_baseline"] = cpu()
             sec.append(entry)
             progress(f"{name}: {entry['ms']} ms")
 
@@ -203,11 +234,13 @@ def main():
             t1 = torch.empty(max(tb, 1), dtype=torch.uint8, device="cuda")
             add("DeviceReduce::Sum int32 N=2^28", 4 * n + 4,
                 lambda: chk(L.lcpp_reduce_sum(I32, ctypes.c_void_p(t1.data_ptr()), tb, ctypes.c_void_p(x.data_ptr()),
-                                              ctypes.c_void_p(o1.data_ptr()), n, sp), "reduce"), 20, "reduce_partials")
+                                              ctypes.c_void_p(o1.data_ptr()), n, sp), "reduce"), 20, "reduce_partials",
+                cpu=lambda: cpu_reduce(1 << 26))
             n24 = 1 << 24
             add("DeviceReduce::Sum int32 N=2^24 (configs[0])", 4 * n24 + 4,
                 lambda: chk(L.lcpp_reduce_sum(I32, ctypes.c_void_p(t1.data_ptr()), tb, ctypes.c_void_p(x.data_ptr()),
-                                              ctypes.c_void_p(o1.data_ptr()), n24, sp), "reduce"), 50, "reduce_partials")
+                                              ctypes.c_void_p(o1.data_ptr()), n24, sp), "reduce"), 30,
+                "reduce_partials", cpu=lambda: cpu_reduce(n24), flushed=True)
             ta = tmp_bytes(L.lcpp_reduce_arg_temp_bytes, I32, n)
             t2 = torch.empty(max(ta, 1), dtype=torch.uint8, device="cuda")
             ix = torch.empty(1, dtype=torch.int32, device="cuda")
@@ -225,14 +258,16 @@ def main():
             add("DeviceScan::ExclusiveSum uint32 N=2^28", 8 * n,
                 lambda: chk(L.lcpp_scan_exclusive_sum(U32, ctypes.c_void_p(t1.data_ptr()), tb,
                                                       ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
-                                                      n, sp), "scan"), 20, "scan_exclusive")
+                                                      n, sp), "scan"), 20, "scan_exclusive",
+                cpu=lambda: cpu_scan("u8_u32", False, 1 << 26))
             del x
             xf = datagen.normal_f32(n)
             yf = torch.empty_like(xf)
             add("DeviceScan::InclusiveSum float32 N=2^28", 8 * n,
                 lambda: chk(L.lcpp_scan_inclusive_sum(F32, ctypes.c_void_p(t1.data_ptr()), tb,
                                                       ctypes.c_void_p(xf.data_ptr()), ctypes.c_void_p(yf.data_ptr()),
-                                                      n, sp), "scan"), 20, "scan_inclusive")
+                                                      n, sp), "scan"), 20, "scan_inclusive",
+                cpu=lambda: cpu_scan("normal_f32", True, 1 << 26))
             del xf, yf, y, t1
         if want("sort_and3"):
             n = 1 << 28
@@ -243,26 +278,39 @@ def main():
             add("DeviceRadixSort::SortKeys uint32 N=2^28 AND-of-3 (low entropy)", 36 * n,
                 lambda: chk(L.lcpp_radix_sort_keys(U32, ctypes.c_void_p(t1.data_ptr()), tb,
                                                    ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(ko.data_ptr()), n,
-                                                   sp), "sort"), 10, "rs_onesweep", items=n)
+                                                   sp), "sort"), 10, "rs_onesweep", items=n,
+                cpu=lambda: cpu_sort("keys_u32_and3", 1 << 25))
             del k, ko, t1
         if want("pairs"):
             n = 1 << 27
-            k = datagen.keys_u64_low16(n)
             v = datagen.iota_u32(n)
-            ko, vo = torch.empty_like(k), torch.empty_like(v)
+            vo = torch.empty_like(v)
             tb = tmp_bytes(L.lcpp_radix_sort_pairs_temp_bytes, U64, U32, n)
             t1 = torch.empty(tb, dtype=torch.uint8, device="cuda")
-            # 16 random low bits: passes 2..7 see one digit for every key and are
-            # skipped (identity permutations), so the bytes counted are the
-            # histogram (8 B) plus the two passes that move data (2 x 24 B); the
-            # reference's eight passes would move 200 B per pair
-            add("DeviceRadixSort::SortPairs uint64->uint32 N=2^27 (16 random low bits; 2 of 8 digit passes move data)",
-                56 * n,
-                lambda: chk(L.lcpp_radix_sort_pairs(U64, U32, ctypes.c_void_p(t1.data_ptr()), tb,
-                                                    ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(ko.data_ptr()),
-                                                    ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(vo.data_ptr()),
-                                                    n, sp), "pairs"), 5, "rs_onesweep", items=n)
-            del k, v, ko, vo, t1
+            for full in (False, True):
+                k = datagen.keys_u64(n) if full else datagen.keys_u64_low16(n)
+                ko = torch.empty_like(k)
+
+                def call(k=k, ko=ko):
+                    chk(L.lcpp_radix_sort_pairs(U64, U32, ctypes.c_void_p(t1.data_ptr()), tb,
+                                                ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(ko.data_ptr()),
+                                                ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(vo.data_ptr()), n, sp),
+                        "pairs")
+                if full:
+                    add("DeviceRadixSort::SortPairs uint64->uint32 N=2^27, keys over the full 64-bit range "
+                        "(all 8 digit passes move data)", 200 * n, call, 5, "rs_onesweep", items=n,
+                        note="200 B per pair: histogram 8 + 8 passes x (8 + 4 read, 8 + 4 written)")
+                else:
+                    # 16 random low bits: passes 2..7 see one digit for every key and are
+                    # skipped (identity permutations), so the bytes counted are the
+                    # histogram (8 B) plus the two passes that move data (2 x 24 B)
+                    add("DeviceRadixSort::SortPairs uint64->uint32 N=2^27 (configs[3]: 16 random low bits; "
+                        "2 of 8 digit passes move data)", 56 * n, call, 5, "rs_onesweep", items=n,
+                        cpu=lambda: cpu_pairs(1 << 24),
+                        note="56 B per pair counted: the 6 passes whose digit every key shares are skipped; "
+                             "the full-range entry times 8 moving passes")
+                del k, ko
+            del v, vo, t1
         if want("by_key"):
             n = 1 << 28
             k = datagen.run_keys_i32(n, 7)
@@ -301,51 +349,109 @@ def main():
                 lambda: chk(L.lcpp_segment_reduce_sum(F32, None, 0, ctypes.c_void_p(x.data_ptr()),
                                                       ctypes.c_void_p(y.data_ptr()), S, ctypes.c_void_p(db.data_ptr()),
                                                       ctypes.c_void_p(de.data_ptr()), sp), "segment"), 20,
-                "segment_reduce")
+                "segment_reduce", cpu=lambda: cpu_segment(n, S, b, e))
             del x, y, db, de
+        del flush_buf
         result["secondary"] = sec
 
     # ------------------------------------------------------------ CPU baseline (oracle onesweep port)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_sort("keys_u32", 1 << 25, seed=0xC3A)
         progress(f"cpu baseline: {result['cpu_baseline']['value']} Gkeys/s")
 
     print(json.dumps(result), flush=True)
 
 
-def cpu_baseline():
-    import numpy as np
+# ---------------------------------------------------------------- CPU baselines
+# The reference's own CPU path (LuisaCompute's fallback backend) cannot be built:
+# LuisaCompute is not vendored and the reference's CMake disables that backend.
+# These time the oracle's C restatements of the reference algorithms (same tile
+# decomposition, look-back across threads) on this host, on bounded samples of
+# each configuration; median of 3 after 1 warm-up.
 
-    from oracle import oracle as o
+def _threads():
+    return max(1, min(len(os.sched_getaffinity(0)), 16))  # the GPU box's CPU share is 16 threads
 
-    cores = len(os.sched_getaffinity(0))
-    threads = max(1, min(cores, 16))  # the GPU box's CPU share is 16 threads
-    n = 1 << 25
-    keys = o.gen("keys_u32", n, 0xC3A)
-    o.radix_sort(keys[: 1 << 20], nthreads=threads)  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        o.radix_sort(keys, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    model = ""
+
+def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {
-        "value": round(n / med / 1e9, 4),
-        "unit": "Gkeys/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"SortKeys uint32 N=2^25 uniform (same generator), 4 x 8-bit onesweep passes with an "
-                  f"atomic look-back across {threads} threads; median of 3 after 1 warm-up; host CPU: {model}",
-    }
+    return ""
+
+
+def _median_s(fn):
+    fn()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def _entry(value, unit, sample):
+    return {"value": round(value, 4), "unit": unit, "cores": _threads(), "kind": "port",
+            "sample": f"{sample}; {_threads()} threads; median of 3 after 1 warm-up; host CPU: {_cpu_model()}"}
+
+
+def _log2(n):
+    return n.bit_length() - 1
+
+
+def cpu_reduce(n):
+    from oracle import oracle as o
+
+    a = o.gen("reduce_i32", n, 0xC1)
+    s = _median_s(lambda: o.reduce(o.OP_SUM, a, nthreads=_threads()))
+    return _entry(4 * n / s / 1e9, "GB/s",
+                  f"DeviceReduce::Sum int32 N=2^{_log2(n)} (same generator), per-thread chunks + one fold")
+
+
+def cpu_scan(kind, inclusive, n):
+    from oracle import oracle as o
+
+    a = o.gen(kind, n, 0xC2B if kind == "normal_f32" else 0xC2A)
+    s = _median_s(lambda: o.scan(a, inclusive, nthreads=_threads()))
+    return _entry(8 * n / s / 1e9, "GB/s",
+                  f"DeviceScan::{'In' if inclusive else 'Ex'}clusiveSum {a.dtype} N=2^{_log2(n)} (same generator), "
+                  f"16384-item tiles, decoupled look-back across threads")
+
+
+def cpu_sort(kind, n, seed=None):
+    from oracle import oracle as o
+
+    seeds = (0xC3B1, 0xC3B2, 0xC3B3) if kind == "keys_u32_and3" else (seed or 0xC3A,)
+    keys = o.gen(kind, n, *seeds)
+    s = _median_s(lambda: o.radix_sort(keys, nthreads=_threads()))
+    return _entry(n / s / 1e9, "Gkeys/s",
+                  f"SortKeys uint32 N=2^{_log2(n)} ({kind}, same generator), histogram + 4 x 8-bit onesweep "
+                  f"passes, atomic look-back across threads")
+
+
+def cpu_pairs(n):
+    from oracle import oracle as o
+
+    keys = o.gen("keys_u64_low16", n, 0xC4)
+    vals = o.gen("iota_u32", n)
+    s = _median_s(lambda: o.radix_sort(keys, vals, nthreads=_threads()))
+    return _entry(n / s / 1e9, "Gpairs/s",
+                  f"SortPairs uint64 (16 random low bits) -> uint32 N=2^{_log2(n)} (same generator), all 8 "
+                  f"onesweep passes, as the reference runs them")
+
+
+def cpu_segment(n, S, b, e):
+    from oracle import oracle as o
+
+    a = o.gen("normal_f32", n, 0xC5)
+    s = _median_s(lambda: o.segment_reduce_mt(a, b, e, _threads()))
+    return _entry((4 * n + 12 * S) / s / 1e9, "GB/s",
+                  f"DeviceSegmentReduce::Sum float32 N=2^{_log2(n)} S=2^{_log2(S)} (the full configuration), "
+                  f"segments split over threads")
 
 
 if __name__ == "__main__":

@@ -27,7 +27,7 @@ __host__ __device__ __forceinline__ uint64_t word(uint64_t seed, uint64_t i)
     return mix64(seed + (i + 1) * kGamma);
 }
 
-enum Gen { kReduceI32, kU8U32, kNormalF32, kKeysU32, kKeysAnd3, kKeysU64Low16, kIotaU32 };
+enum Gen { kReduceI32, kU8U32, kNormalF32, kKeysU32, kKeysAnd3, kKeysU64Low16, kIotaU32, kKeysU64 };
 
 template <int G>
 __global__ __launch_bounds__(256) void gen_kernel(void *out, uint64_t n, uint64_t s0, uint64_t s1,
@@ -53,6 +53,8 @@ __global__ __launch_bounds__(256) void gen_kernel(void *out, uint64_t n, uint64_
                 (uint32_t)word(s0, i) & (uint32_t)word(s1, i) & (uint32_t)word(s2, i);
         } else if constexpr (G == kKeysU64Low16) {
             static_cast<uint64_t *>(out)[i] = word(s0, i) & 0xFFFFull;
+        } else if constexpr (G == kKeysU64) {
+            static_cast<uint64_t *>(out)[i] = word(s0, i);
         } else {
             static_cast<uint32_t *>(out)[i] = (uint32_t)i;
         }
@@ -251,6 +253,10 @@ int lcpp_gen_keys_u32_and3(uint64_t sa, uint64_t sb, uint64_t sc, uint64_t n, vo
 int lcpp_gen_keys_u64_low16(uint64_t seed, uint64_t n, void *out, void *stream)
 {
     return launch<kKeysU64Low16>(out, n, seed, 0, 0, stream);
+}
+int lcpp_gen_keys_u64(uint64_t seed, uint64_t n, void *out, void *stream)
+{
+    return launch<kKeysU64>(out, n, seed, 0, 0, stream);
 }
 int lcpp_gen_iota_u32(uint64_t n, void *out, void *stream)
 {

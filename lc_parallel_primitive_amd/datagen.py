@@ -33,7 +33,7 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(lib_path)
         u64, vp, i = ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
         for name in ("lcpp_gen_reduce_i32", "lcpp_gen_u8_u32", "lcpp_gen_normal_f32", "lcpp_gen_keys_u32",
-                     "lcpp_gen_keys_u64_low16"):
+                     "lcpp_gen_keys_u64_low16", "lcpp_gen_keys_u64"):
             f = getattr(L, name)
             f.restype, f.argtypes = i, [u64, u64, vp, vp]
         L.lcpp_gen_keys_u32_and3.restype = i
@@ -116,6 +116,18 @@ def keys_u64_low16(n: int, seed: int = SEED_PAIRS_U64, device="cuda"):
 
     t = torch.empty(n, dtype=torch.uint64, device=device)
     _run(lib().lcpp_gen_keys_u64_low16(seed, n, t.data_ptr(), _stream()), "gen_keys_u64_low16")
+    return t
+
+
+SEED_PAIRS_U64_FULL = 0xC48
+
+
+def keys_u64(n: int, seed: int = SEED_PAIRS_U64_FULL, device="cuda"):
+    """k_i = w_i: uniform over the full 64-bit range (every onesweep pass moves data)."""
+    import torch
+
+    t = torch.empty(n, dtype=torch.uint64, device=device)
+    _run(lib().lcpp_gen_keys_u64(seed, n, t.data_ptr(), _stream()), "gen_keys_u64")
     return t
 
 

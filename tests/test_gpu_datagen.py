@@ -17,6 +17,7 @@ def test_generators_match_host(gpu):
     assert (g.to_host(dg.keys_u32(n)) == o.gen("keys_u32", n, dg.SEED_SORT_U32)).all()
     assert (g.to_host(dg.keys_u32_and3(n)) == o.gen("keys_u32_and3", n, *dg.SEED_SORT_AND3)).all()
     assert (g.to_host(dg.keys_u64_low16(n)) == o.gen("keys_u64_low16", n, dg.SEED_PAIRS_U64)).all()
+    assert (g.to_host(dg.keys_u64(n)) == o.words(dg.SEED_PAIRS_U64_FULL, n)).all()
     assert (g.to_host(dg.iota_u32(n)) == np.arange(n, dtype=np.uint32)).all()
     # Box-Muller in double through the device libm: equal after rounding to float32
     # except for rare last-ulp differences of log/cos

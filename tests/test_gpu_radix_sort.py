@@ -209,6 +209,20 @@ def test_full_size_pairs_u64_index(gpu):
     assert o.check_stable_pairs_u64_u32(g.to_host(k), g.to_host(ko), g.to_host(vo))
 
 
+def test_full_size_pairs_u64_full_range_8_passes(gpu):
+    # C4's shape with keys over the full 64-bit range: no digit pass is
+    # trivial, so all 8 onesweep passes move keys and values
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 27
+    log("sort pairs u64 (full range)/u32 2^27, 8 passes")
+    k = datagen.keys_u64(n)
+    v = datagen.iota_u32(n)
+    ko, vo = sort_pairs(k, v, n, np.uint64, np.uint32)
+    assert o.check_stable_pairs_u64_u32(g.to_host(k), g.to_host(ko), g.to_host(vo))
+
+
 def test_full_size_u32_descending(gpu):
     # C3a input sorted with SortKeysDescending: the reversed output must be an
     # ascending permutation of the input
