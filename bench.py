@@ -62,6 +62,9 @@ def parse():
     ap.add_argument("--only", default=None, help="run one secondary workload by name (profiling)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 2^28 x uint32 streaming copy (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--copy-shapes", action="store_true",
+                    help="only time 2^28 x uint32 copies in the access shapes of the scan and onesweep kernels "
+                         "(the ceilings those shapes allow)")
     return ap.parse_args()
 
 
@@ -123,6 +126,22 @@ def main():
         print(json.dumps({"copy_probe": {"bytes_read_per_launch": 4 * n, "bytes_written_per_launch": 4 * n,
                                          "launches": args.steps + args.warmup, "ms": round(ms, 4),
                                          "GB/s": round(8 * n / (ms * 1e-3) / 1e9, 1)}}), flush=True)
+        return
+
+    if args.copy_shapes:
+        rows = {}
+        for shape, what in datagen.COPY_SHAPES.items():
+            n = 1 << 28
+            if shape in (1, 2):
+                n -= n % 20480
+            src = datagen.keys_u32(n)
+            dst = torch.empty_like(src)
+            ms = timed(lambda: datagen.copy_shape(src, dst, shape), args.steps, args.warmup)
+            gbs = 8 * n / (ms * 1e-3) / 1e9
+            rows[shape] = {"shape": what, "n": n, "us": round(ms * 1e3, 1), "GB/s": round(gbs, 1),
+                           "frac": round(gbs / 8000, 3)}
+            print(json.dumps({"copy_shape": shape, **rows[shape]}), flush=True)
+            del src, dst
         return
 
     # ------------------------------------------------------------ headline: SortKeys u32 2^28

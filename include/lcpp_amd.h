@@ -36,7 +36,17 @@ extern "C" {
 
 #define LCPP_AMD_VERSION 100 /* 1.0.0 */
 
-typedef enum lcpp_dtype {
+/* The enums are int-sized in C.  C++ fixes int as their underlying type, so
+ * that every int a C, Go or Python caller passes is a value of the enum type
+ * in the library (which rejects unknown codes with a status instead of
+ * reading an out-of-range enum). */
+#ifdef __cplusplus
+#define LCPP_ENUM_INT : int
+#else
+#define LCPP_ENUM_INT
+#endif
+
+typedef enum lcpp_dtype LCPP_ENUM_INT {
     LCPP_INT32 = 0,
     LCPP_UINT32 = 1,
     LCPP_FLOAT32 = 2,
@@ -47,20 +57,20 @@ typedef enum lcpp_dtype {
 
 /* Reduction operators and element transforms of lcpp_reduce_transform (the
  * reference takes arbitrary device functors; a C ABI carries a fixed set). */
-typedef enum lcpp_reduce_op {
+typedef enum lcpp_reduce_op LCPP_ENUM_INT {
     LCPP_OP_SUM = 0,
     LCPP_OP_MIN = 1,
     LCPP_OP_MAX = 2
 } lcpp_reduce_op;
 
-typedef enum lcpp_transform {
+typedef enum lcpp_transform LCPP_ENUM_INT {
     LCPP_XFORM_IDENTITY = 0,
     LCPP_XFORM_NEGATE = 1, /* integers wrap (two's complement) */
     LCPP_XFORM_ABS = 2,    /* identity for unsigned types */
     LCPP_XFORM_SQUARE = 3  /* integers wrap */
 } lcpp_transform;
 
-typedef enum lcpp_status {
+typedef enum lcpp_status LCPP_ENUM_INT {
     LCPP_OK = 0,
     LCPP_ERR_INVALID_ARG = -1,      /* null pointer, misaligned temp, size out of range */
     LCPP_ERR_TEMP_TOO_SMALL = -2,   /* temp_bytes < the *_temp_bytes query result */

@@ -358,7 +358,8 @@ WaitCtl wait_ctl(uint32_t *status);
 
 // ---------------------------------------------------------------- misc
 
-__host__ __device__ constexpr uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+// (no a + b - 1 that would wrap for sizes near 2^64)
+__host__ __device__ constexpr uint64_t ceil_div(uint64_t a, uint64_t b) { return a / b + (a % b != 0); }
 __host__ __device__ constexpr uint64_t align_up(uint64_t a, uint64_t b) { return ceil_div(a, b) * b; }
 
 // Host-side launch bookkeeping (profile.cpp): brackets a launch with HIP

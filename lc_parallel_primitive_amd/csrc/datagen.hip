@@ -181,9 +181,133 @@ __global__ __launch_bounds__(256) void lds_order_probe_kernel(uint64_t seed, uin
     if (bad) atomicAdd(violations, (unsigned long long)bad);
 }
 
+// ---------------------------------------------------------------- copy shapes
+// Pure permutation copies of n uint32 (read 4n, write 4n bytes) in the access
+// shapes of the primitives' kernels, so each kernel can be compared with what
+// its own shape achieves as a copy.  Occupancy is pinned with unused dynamic
+// LDS where the shape says so, to the workgroups per CU of the kernel it stands
+// for (a copy needs fewer registers than the kernel and would otherwise run
+// more workgroups per CU):
+//   1      the exclusive scan's tile: one 256-thread workgroup per tile of 20
+//          16-byte vectors per thread held in registers, non-temporal loads
+//          and stores; 4 workgroups per CU (36 KiB LDS each).
+//   2      as 1 with the copy's own occupancy.
+//   3      a grid-stride loop of 16-byte vectors over 2048 workgroups.
+//   4      the onesweep's tile: 512 threads x 32 wave-striped dword loads, then
+//          32 dword stores, thread-striped over the tile; 3 workgroups per CU
+//          (48 KiB LDS each).
+//   5..8   the onesweep's tile (as 4) writing its keys as if sorted into 256
+//          digit runs of 64 keys (256 B) each, every tile's run of digit d
+//          following the previous tile's (positions d * n/256 + tile * 64 + ..):
+//          5  runs line-aligned, XCD runs of 16 tiles (the sort's workgroup ->
+//             tile map);
+//          6  run boundaries inside cache lines (digit pairs 2k, 2k+1 split
+//             their 128 slots at 64 +- a_k, mirrored by odd tiles, so runs stay
+//             contiguous across tiles), XCD runs of 16;
+//          7  as 6 with plain dispatch order (runs of 1);
+//          8  line-aligned runs, but every store instruction straddles lines
+//             whose other half comes from the neighbouring wave of the same tile.
+// Shape 0 is copy_probe_kernel above.  n must be a multiple of 16384 and at
+// least 65536 (shapes 4-8), or a multiple of 20480 (shapes 1, 2).
+__device__ __forceinline__ uint32_t dg_xcd_tile(uint32_t b, uint32_t grid, uint32_t log_run)
+{
+    const uint32_t log_group = log_run + 3;
+    const uint32_t g = b >> log_group;
+    if ((g + 1) << log_group > grid) return b;
+    const uint32_t r = b & ((1u << log_group) - 1);
+    return (g << log_group) + ((r & 7) << log_run) + (r >> 3);
+}
+
+template <int VECS>
+__global__ __launch_bounds__(256) void shape_scan_tile(const u32x4c *__restrict__ in, u32x4c *__restrict__ out)
+{
+    const uint64_t base = (uint64_t)blockIdx.x * 256 * VECS;
+    u32x4c v[VECS];
+#pragma unroll
+    for (int k = 0; k < VECS; ++k) v[k] = __builtin_nontemporal_load(in + base + (uint64_t)k * 256 + threadIdx.x);
+    __syncthreads();  // the whole tile is in registers before the first store, as in the scan
+#pragma unroll
+    for (int k = 0; k < VECS; ++k) __builtin_nontemporal_store(v[k], out + base + (uint64_t)k * 256 + threadIdx.x);
+}
+
+__global__ __launch_bounds__(256) void shape_grid_stride(const u32x4c *__restrict__ in, u32x4c *__restrict__ out,
+                                                         uint64_t nvec)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += (uint64_t)gridDim.x * 256)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(in + i), out + i);
+}
+
+// Output position of sorted slot i of `tile` in shapes 4..8 (see above).
+__device__ __forceinline__ uint32_t shape_pos(int shape, uint32_t tile, uint32_t i, uint32_t n)
+{
+    const uint32_t region = n >> 8;
+    if (shape == 4) return tile * 16384u + i;
+    if (shape == 5) return (i >> 6) * region + tile * 64u + (i & 63u);
+    if (shape == 8) {
+        const uint32_t i2 = (i + 16u) & 16383u;
+        return (i2 >> 6) * region + tile * 64u + (i2 & 63u);
+    }
+    const uint32_t kk = i >> 7, r = i & 127u;
+    const uint32_t a = (kk * 37u) % 29u + 1u;
+    const bool odd = tile & 1u;
+    const uint32_t split = odd ? 64u - a : 64u + a;
+    const uint32_t d = r < split ? 2 * kk : 2 * kk + 1;
+    const uint32_t within = r < split ? r : r - split;
+    const uint32_t pre = tile * 64u + (odd ? ((d & 1u) ? 0u - a : a) : 0u);
+    return d * region + pre + within;
+}
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6, 6)))
+void shape_onesweep_tile(const uint32_t *__restrict__ in, uint32_t *__restrict__ out, uint32_t n, int shape,
+                         uint32_t log_run)
+{
+    const uint32_t tile = dg_xcd_tile(blockIdx.x, gridDim.x, log_run);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t base = tile * 16384u;
+    uint32_t k[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) k[u] = __builtin_nontemporal_load(in + base + wave * 2048u + (uint32_t)u * 64u + lane);
+    __syncthreads();  // the tile is loaded before it is written, as in the onesweep
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const uint32_t p = shape_pos(shape, tile, (uint32_t)j * 512u + tid, n);
+        if (p < n) out[p] = k[j];
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+int lcpp_copy_probe_u32(const void *in, void *out, uint64_t n, void *stream);
+
+// Copy of n uint32 in access shape `shape` (0..8, see the copy shapes above);
+// 16-byte aligned pointers.  Shapes 0-3 copy in[i] to out[i]; 4-8 permute.  Returns -1 for a shape or size it does not take.
+int lcpp_dg_copy_shape(const void *in, void *out, uint64_t n, int shape, void *stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!in || !out || ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15)) return -1;
+    if (n > 0xFFFFFFFFull) return -1;
+    const auto *vi = static_cast<const u32x4c *>(in);
+    auto *vo = static_cast<u32x4c *>(out);
+    if (shape == 0) return lcpp_copy_probe_u32(in, out, n, stream);
+    if (shape == 1 || shape == 2) {
+        if (n % (256 * 20 * 4)) return -1;
+        shape_scan_tile<20><<<(uint32_t)(n / (256 * 20 * 4)), 256, shape == 1 ? 36u << 10 : 0u, s>>>(vi, vo);
+    } else if (shape == 3) {
+        if (n % 4) return -1;
+        shape_grid_stride<<<2048, 256, 0, s>>>(vi, vo, n / 4);
+    } else if (shape >= 4 && shape <= 8) {
+        if (n % 16384 || n < 65536) return -1;
+        const uint32_t log_run = shape == 4 || shape == 7 ? 0u : 4u;
+        shape_onesweep_tile<<<(uint32_t)(n / 16384), 512, 48u << 10, s>>>(static_cast<const uint32_t *>(in),
+                                                                   static_cast<uint32_t *>(out), (uint32_t)n, shape,
+                                                                   log_run);
+    } else {
+        return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
 
 // out[3] (device, zeroed by the caller): descents, sum, sum of mix64.
 int lcpp_dg_sorted_hash_u32(const void *a, uint64_t n, void *out, void *stream)

@@ -870,6 +870,7 @@ extern "C" int lcpp_radix_sort_keys_temp_bytes(lcpp_dtype k, uint64_t n, size_t 
     if (!bytes) return LCPP_ERR_INVALID_ARG;
     const int kb = dtype_bytes(k);
     if (!kb) return LCPP_ERR_UNSUPPORTED_DTYPE;
+    if (n > kMaxItems) return LCPP_ERR_INVALID_ARG;  // as the sort itself
     *bytes = rs_layout(n, kb, 0).total;
     return LCPP_OK;
 }
@@ -880,6 +881,7 @@ extern "C" int lcpp_radix_sort_pairs_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint
     if (!bytes) return LCPP_ERR_INVALID_ARG;
     const int kb = dtype_bytes(k), vb = dtype_bytes(v);
     if (!kb || !vb) return LCPP_ERR_UNSUPPORTED_DTYPE;
+    if (n > kMaxItems) return LCPP_ERR_INVALID_ARG;
     *bytes = rs_layout(n, kb, vb).total;
     return LCPP_OK;
 }

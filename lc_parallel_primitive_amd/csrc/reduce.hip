@@ -489,6 +489,7 @@ extern "C" int lcpp_reduce_transform(lcpp_dtype t, lcpp_reduce_op op, lcpp_trans
 extern "C" int lcpp_reduce_arg_temp_bytes(lcpp_dtype t, uint64_t n, size_t *bytes)
 {
     if (!bytes) return LCPP_ERR_INVALID_ARG;
+    if (n > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;  // 32-bit indices, as the call
     switch (t) {
     case LCPP_INT32: case LCPP_UINT32: case LCPP_FLOAT32: *bytes = arg_temp<uint32_t>(n); return LCPP_OK;
     case LCPP_INT64: case LCPP_UINT64: case LCPP_FLOAT64: *bytes = arg_temp<uint64_t>(n); return LCPP_OK;

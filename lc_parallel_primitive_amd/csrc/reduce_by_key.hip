@@ -280,6 +280,7 @@ extern "C" int lcpp_reduce_by_key_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint64_
 {
     if (!bytes) return LCPP_ERR_INVALID_ARG;
     if (!rbk_valid_dtype(k) || !rbk_valid_dtype(v)) return LCPP_ERR_UNSUPPORTED_DTYPE;
+    if (n > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;  // 32-bit run counts, as the call
     *bytes = rbk_wide(v) ? rbk_layout<uint64_t>(n).total : rbk_layout<uint32_t>(n).total;
     return LCPP_OK;
 }

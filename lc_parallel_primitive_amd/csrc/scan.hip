@@ -249,9 +249,16 @@ using namespace lcpp;
 extern "C" int lcpp_scan_temp_bytes(lcpp_dtype t, uint64_t n, size_t *bytes)
 {
     if (!bytes) return LCPP_ERR_INVALID_ARG;
+    // sizes the scans reject (more than 2^32-1 tiles) are rejected here too
     switch (t) {
-    case LCPP_INT32: case LCPP_UINT32: case LCPP_FLOAT32: *bytes = scan_temp_bytes<uint32_t>(n); return LCPP_OK;
-    case LCPP_INT64: case LCPP_UINT64: case LCPP_FLOAT64: *bytes = scan_temp_bytes<uint64_t>(n); return LCPP_OK;
+    case LCPP_INT32: case LCPP_UINT32: case LCPP_FLOAT32:
+        if (scan_tiles<uint32_t, false>(n) > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;
+        *bytes = scan_temp_bytes<uint32_t>(n);
+        return LCPP_OK;
+    case LCPP_INT64: case LCPP_UINT64: case LCPP_FLOAT64:
+        if (scan_tiles<uint64_t, false>(n) > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;
+        *bytes = scan_temp_bytes<uint64_t>(n);
+        return LCPP_OK;
     default: return LCPP_ERR_UNSUPPORTED_DTYPE;
     }
 }

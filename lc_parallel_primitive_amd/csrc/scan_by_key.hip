@@ -221,8 +221,9 @@ extern "C" int lcpp_scan_by_key_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint64_t 
 {
     if (!bytes) return LCPP_ERR_INVALID_ARG;
     if (!valid_dtype(k) || !valid_dtype(v)) return LCPP_ERR_UNSUPPORTED_DTYPE;
-    *bytes = (v == LCPP_INT64 || v == LCPP_UINT64 || v == LCPP_FLOAT64) ? sbk_temp_bytes<uint64_t>(n)
-                                                                         : sbk_temp_bytes<uint32_t>(n);
+    const bool wide = v == LCPP_INT64 || v == LCPP_UINT64 || v == LCPP_FLOAT64;
+    if ((wide ? bk_tiles<uint64_t>(n) : bk_tiles<uint32_t>(n)) > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;
+    *bytes = wide ? sbk_temp_bytes<uint64_t>(n) : sbk_temp_bytes<uint32_t>(n);
     return LCPP_OK;
 }
 

@@ -42,6 +42,8 @@ def lib() -> ctypes.CDLL:
         L.lcpp_gen_iota_u32.argtypes = [u64, vp, vp]
         L.lcpp_copy_probe_u32.restype = i
         L.lcpp_copy_probe_u32.argtypes = [vp, vp, u64, vp]
+        L.lcpp_dg_copy_shape.restype = i
+        L.lcpp_dg_copy_shape.argtypes = [vp, vp, u64, ctypes.c_int, vp]
         L.lcpp_gen_segments_host.restype = i
         L.lcpp_gen_segments_host.argtypes = [u64, u64, u64, u64, vp, vp]
         L.lcpp_dg_sorted_hash_u32.restype = i
@@ -172,6 +174,67 @@ def copy_probe(src, dst):
     n = src.numel()
     _run(lib().lcpp_copy_probe_u32(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), n, _stream()),
          "copy_probe")
+
+
+COPY_SHAPES = {
+    0: "streaming copy, 16-byte vectors, 2 per thread",
+    1: "scan tile: 256 thr x 20 x 16 B in registers, 4 WG/CU",
+    2: "scan tile, copy's own occupancy",
+    3: "grid-stride 16-byte copy, 2048 WGs",
+    4: "onesweep tile: 512 thr x 32 dwords, sequential stores, 3 WG/CU",
+    5: "onesweep tile -> 256 runs of 256 B, line-aligned, XCD runs of 16",
+    6: "onesweep tile -> 256 runs, boundaries inside lines, XCD runs of 16",
+    7: "onesweep tile -> 256 runs, boundaries inside lines, dispatch order",
+    8: "onesweep tile -> 256 aligned runs, stores straddling lines",
+}
+
+
+def copy_shape(src, dst, shape):
+    """Copy/permutation of a uint32 tensor in one of the access shapes of
+    COPY_SHAPES (ceilings for the kernels that use those shapes)."""
+    _run(lib().lcpp_dg_copy_shape(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), src.numel(), shape,
+                                  _stream()), f"copy_shape {shape}")
+
+
+def copy_shape_positions(n, shape):
+    """numpy restatement of where shapes 4-8 write in[i] (host check of the
+    probe's index arithmetic)."""
+    import numpy as np
+
+    tiles = n // 16384
+    b = np.arange(tiles, dtype=np.int64)
+    log_run = 0 if shape in (4, 7) else 4
+    lg = log_run + 3
+    g, r = b >> lg, b & ((1 << lg) - 1)
+    full = ((g + 1) << lg) <= tiles
+    tile_of_wg = np.where(full, (g << lg) + ((r & 7) << log_run) + (r >> 3), b)
+    tid = np.arange(512, dtype=np.int64)
+    lane, wave = tid & 63, tid >> 6
+    u = np.arange(32, dtype=np.int64)
+    region = n >> 8
+    pos = np.empty(n, dtype=np.int64)
+    for wg in range(tiles):
+        t = int(tile_of_wg[wg])
+        src = t * 16384 + wave[None, :] * 2048 + u[:, None] * 64 + lane[None, :]  # [u, tid]
+        i = u[:, None] * 512 + tid[None, :]
+        if shape == 4:
+            p = t * 16384 + i
+        elif shape == 5:
+            p = (i >> 6) * region + t * 64 + (i & 63)
+        elif shape == 8:
+            i2 = (i + 16) & 16383
+            p = (i2 >> 6) * region + t * 64 + (i2 & 63)
+        else:
+            kk, rr = i >> 7, i & 127
+            a = (kk * 37) % 29 + 1
+            odd = t & 1
+            split = 64 - a if odd else 64 + a
+            d = np.where(rr < split, 2 * kk, 2 * kk + 1)
+            within = np.where(rr < split, rr, rr - split)
+            pre = t * 64 + (np.where(d & 1, -a, a) if odd else 0)
+            p = d * region + pre + within
+        pos[src.ravel()] = p.ravel()
+    return pos
 
 
 # ---------------------------------------------------------------- device-side checkers (tests)

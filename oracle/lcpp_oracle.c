@@ -10,6 +10,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
@@ -408,6 +409,7 @@ int lcor_scan(int inclusive, int dtype, const void *in, void *out, uint64_t n)
 int lcor_scan_f64(int inclusive, int dtype, const void *in, double *out, double *abs_prefix,
                   uint64_t n)
 {
+    if (dtype != LCOR_F32 && dtype != LCOR_F64) return -1;
     double s = 0.0, a = 0.0, c = 0.0;
     for (uint64_t i = 0; i < n; ++i) {
         double x;
@@ -497,12 +499,126 @@ int lcor_lookback_kat(uint32_t num_tiles, int nthreads, int32_t *excl, int32_t *
     return 0;
 }
 
+/* ---------------- bounded look-back with a status word ----------------
+ * The look-back above with this library's failure reporting instead of the
+ * reference's unbounded wait (single_pass_scan_operator.h:96-104, 191-240:
+ * WaitForValid spins while any polled predecessor is INVALID).  A wait polls
+ * `width` predecessors at once (top, top-1, .., top-width+1; words below tile
+ * 0 read as INCLUSIVE 0); the predecessors in range are those up to and
+ * including the nearest INCLUSIVE one.  While one in range is INVALID the
+ * wait re-polls the same window; after `spin_limit` re-polls it gives up:
+ * it ORs LOOKBACK_TIMEOUT (bit 0) into *status and folds what has been
+ * published (an unpublished word reads as 0).  Tile `withhold` never
+ * publishes (the device library's test hook); every wait still ends.
+ * Tiles take tickets in order, as workgroups are dispatched in id order.
+ * Tile t's aggregate is agg[t]; excl/incl receive its prefixes (wrapping
+ * int32 sums). */
+#define LCOR_STATUS_LOOKBACK_TIMEOUT 1u
+typedef struct {
+    _Atomic uint64_t *words;
+    _Atomic uint32_t ticket;
+    _Atomic uint32_t *status;
+    uint32_t num_tiles, withhold, spin_limit, width;
+    const int32_t *agg;
+    int32_t *excl, *incl;
+} lbb_ctx;
+
+static void lbb_publish(lbb_ctx *c, uint32_t t, int32_t v, uint32_t st)
+{
+    if (t == c->withhold) return;
+    atomic_store_explicit(&c->words[t], ((uint64_t)(uint32_t)v << 32) | st, memory_order_release);
+}
+
+static int32_t lbb_wait(lbb_ctx *c, uint32_t tile)
+{
+    uint32_t excl = 0, spins = 0;
+    int64_t top = (int64_t)tile - 1;
+    for (;;) {
+        uint32_t st[64], val[64], stop = c->width - 1;
+        int found = 0, missing = 0;
+        for (uint32_t l = 0; l < c->width; ++l) {
+            const int64_t j = top - (int64_t)l;
+            const uint64_t w = j < 0 ? LB_INCLUSIVE : atomic_load_explicit(&c->words[j], memory_order_acquire);
+            st[l] = (uint32_t)(w & 3u);
+            val[l] = (uint32_t)(w >> 32);
+            if (st[l] == LB_INCLUSIVE && !found) { found = 1; stop = l; }
+        }
+        for (uint32_t l = 0; l <= stop; ++l) missing |= st[l] == LB_INVALID;
+        if (missing) {
+            if (++spins < c->spin_limit) { sched_yield(); continue; }
+            atomic_fetch_or_explicit(c->status, LCOR_STATUS_LOOKBACK_TIMEOUT, memory_order_relaxed);
+        }
+        for (uint32_t l = 0; l <= stop; ++l) excl += val[l];
+        if (found) return (int32_t)excl;
+        top -= c->width;
+    }
+}
+
+static void *lbb_worker(void *p)
+{
+    lbb_ctx *c = (lbb_ctx *)p;
+    for (;;) {
+        const uint32_t t = atomic_fetch_add_explicit(&c->ticket, 1, memory_order_relaxed);
+        if (t >= c->num_tiles) break;
+        const int32_t agg = c->agg[t];
+        int32_t ex = 0;
+        if (t == 0) {
+            lbb_publish(c, 0, agg, LB_INCLUSIVE);
+        } else {
+            lbb_publish(c, t, agg, LB_PARTIAL);
+            ex = lbb_wait(c, t);
+            lbb_publish(c, t, (int32_t)((uint32_t)ex + (uint32_t)agg), LB_INCLUSIVE);
+        }
+        c->excl[t] = ex;
+        c->incl[t] = (int32_t)((uint32_t)ex + (uint32_t)agg);
+    }
+    return NULL;
+}
+
+int lcor_lookback_bounded(const int32_t *agg, uint32_t num_tiles, int nthreads, uint32_t withhold,
+                          uint32_t spin_limit, uint32_t width, int32_t *excl, int32_t *incl, uint32_t *status)
+{
+    if (nthreads < 1 || width < 1 || width > 64 || spin_limit < 1 || !status) return -1;
+    if (nthreads > 256) nthreads = 256;
+    lbb_ctx c;
+    c.words = (_Atomic uint64_t *)calloc(num_tiles ? num_tiles : 1, sizeof(uint64_t));
+    if (!c.words) return -1;
+    _Atomic uint32_t st;
+    atomic_init(&st, 0);
+    atomic_init(&c.ticket, 0);
+    c.status = &st;
+    c.num_tiles = num_tiles;
+    c.withhold = withhold;
+    c.spin_limit = spin_limit;
+    c.width = width;
+    c.agg = agg;
+    c.excl = excl;
+    c.incl = incl;
+    pthread_t th[256];
+    int started = 0;
+    for (; started < nthreads; ++started)
+        if (pthread_create(&th[started], NULL, lbb_worker, &c) != 0) break;
+    if (started == 0) lbb_worker(&c);
+    for (int t = 0; t < started; ++t) pthread_join(th[t], NULL);
+    free((void *)c.words);
+    *status = atomic_load(&st);
+    return 0;
+}
+
 /* ---------------- multithreaded single-pass scan (CPU baseline) -------
  * Same tile decomposition as the reference (device/details/scan.h:59-147):
  * tile = ticket, aggregate, look-back, then the tile's scan seeded with the
  * exclusive prefix.  Values are kept in the element type (wrapping for
  * integers). */
 #define SCAN_MT_TILE 16384u
+/* Sanitizer self-test: built with LCOR_PLANT_RELAXED_PUBLISH, the status
+ * stores that publish a tile's values lose their release ordering, a planted
+ * race that the TSan run must report (oracle/Makefile, tsan-planted). */
+#ifdef LCOR_PLANT_RELAXED_PUBLISH
+#define SCAN_MT_PUBLISH memory_order_relaxed
+#else
+#define SCAN_MT_PUBLISH memory_order_release
+#endif
 typedef struct {
     int inclusive, dtype;
     const char *in;
@@ -527,7 +643,7 @@ static void *scan_mt_worker(void *p)
         fold_any(LCOR_OP_SUM, c->dtype, c->in + b * es, e - b, &agg);
         if (t > 0) {
             c->partial[t] = agg;
-            atomic_store_explicit(&c->status[t], LB_PARTIAL, memory_order_release);
+            atomic_store_explicit(&c->status[t], LB_PARTIAL, SCAN_MT_PUBLISH);
             for (int64_t j = (int64_t)t - 1; j >= 0; --j) {
                 uint32_t s;
                 do { s = atomic_load_explicit(&c->status[j], memory_order_acquire); } while (s == LB_INVALID);
@@ -539,7 +655,7 @@ static void *scan_mt_worker(void *p)
         uint64_t inc = prefix;
         fold_any(LCOR_OP_SUM, c->dtype, &agg, 1, &inc);
         c->inclusive_v[t] = inc;
-        atomic_store_explicit(&c->status[t], LB_INCLUSIVE, memory_order_release);
+        atomic_store_explicit(&c->status[t], LB_INCLUSIVE, SCAN_MT_PUBLISH);
         scan_any(c->inclusive, c->dtype, c->in + b * es, c->out + b * es, e - b, &prefix);
     }
     return NULL;

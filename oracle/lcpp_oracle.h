@@ -92,6 +92,11 @@ int lcor_scan_f64(int inclusive, int dtype, const void *in, double *out, double 
                   uint64_t n);
 int lcor_scan_mt(int inclusive, int dtype, const void *in, void *out, uint64_t n, int nthreads);
 int lcor_lookback_kat(uint32_t num_tiles, int nthreads, int32_t *excl, int32_t *incl);
+/* Look-back over per-tile aggregates with bounded waits (windows of `width`
+ * predecessors, give-up after `spin_limit` re-polls, tile `withhold` never
+ * publishes; UINT32_MAX withholds none).  *status gets bit 0 if a wait gave up. */
+int lcor_lookback_bounded(const int32_t *agg, uint32_t num_tiles, int nthreads, uint32_t withhold,
+                          uint32_t spin_limit, uint32_t width, int32_t *excl, int32_t *incl, uint32_t *status);
 
 /* ---------------- radix sort (onesweep restatement) -------------------- */
 int lcor_radix_sort(int key_dtype, int val_bytes, const void *keys_in, void *keys_out,

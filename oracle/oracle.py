@@ -60,6 +60,7 @@ def lib() -> ctypes.CDLL:
             "lcor_scan_f64": (i, [i, i, vp, vp, vp, u64]),
             "lcor_scan_mt": (i, [i, i, vp, vp, u64, i]),
             "lcor_lookback_kat": (i, [u32, i, vp, vp]),
+            "lcor_lookback_bounded": (i, [vp, u32, i, u32, u32, u32, vp, vp, ctypes.POINTER(u32)]),
             "lcor_radix_sort": (i, [i, i, vp, vp, vp, vp, u64, i, i, u32]),
             "lcor_check_stable_pairs_u64_u32": (i, [vp, vp, vp, u64]),
             "lcor_check_sorted_permutation_u32": (i, [vp, vp, u64]),
@@ -197,6 +198,19 @@ def lookback_kat(num_tiles: int, nthreads: int):
     inc = np.empty(num_tiles, np.int32)
     _ok(lib().lcor_lookback_kat(num_tiles, nthreads, _p(ex), _p(inc)), "lookback_kat")
     return ex, inc
+
+
+def lookback_bounded(agg: np.ndarray, nthreads: int, withhold: int = 0xFFFFFFFF, spin_limit: int = 1 << 20,
+                     width: int = 16):
+    """(exclusive, inclusive, status word) of the bounded look-back over the
+    per-tile aggregates `agg` (int32, wrapping); tile `withhold` never publishes."""
+    agg = np.ascontiguousarray(agg, dtype=np.int32)
+    ex = np.empty(agg.size, np.int32)
+    inc = np.empty(agg.size, np.int32)
+    st = ctypes.c_uint32(0)
+    _ok(lib().lcor_lookback_bounded(_p(agg), agg.size, nthreads, withhold, spin_limit, width, _p(ex), _p(inc),
+                                    ctypes.byref(st)), "lookback_bounded")
+    return ex, inc, st.value
 
 
 # ---------------------------------------------------------------- sort

@@ -49,3 +49,27 @@ def test_run_keys_match_host(gpu):
     n = 300_007
     w = o.gen("keys_u32", n, dg.SEED_BY_KEY)
     assert (g.to_host(dg.run_keys_i32(n, 7)) == np.cumsum((w & 127) == 0, dtype=np.int32)).all()
+
+
+@pytest.mark.parametrize("shape", range(9))
+def test_copy_shapes_write_where_stated(gpu, shape):
+    """The copy-shape probes (ceilings quoted for the scan and onesweep kernels)
+    move every word: shapes 0-3 copy in place, 4-8 write in[i] to the position
+    the host restatement gives; the guard past n stays untouched."""
+    import torch
+
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen as dg
+
+    n = 20480 * 100 if shape in (1, 2) else 1 << 21  # 128 onesweep tiles: one full XCD group of 16-runs
+    src = torch.arange(n + 64, dtype=torch.int32, device="cuda").view(torch.uint32)
+    dst = torch.full((n + 64,), -1, dtype=torch.int32, device="cuda").view(torch.uint32)
+    dg.copy_shape(src[:n], dst[:n], shape)
+    h = g.to_host(dst.view(torch.int32))
+    assert (h[n:] == -1).all()
+    if shape <= 3:
+        assert (h[:n] == np.arange(n)).all()
+    else:
+        expect = np.empty(n, dtype=np.int32)
+        expect[dg.copy_shape_positions(n, shape)] = np.arange(n, dtype=np.int32)
+        assert (h[:n] == expect).all()

@@ -198,6 +198,42 @@ def test_lookback_kat_102400_tiles():
     assert (ex == np.arange(102400)).all() and (inc == np.arange(1, 102401)).all()
 
 
+@pytest.mark.parametrize("nthreads", [1, 4, 8])
+@pytest.mark.parametrize("width", [1, 16, 64])
+def test_bounded_lookback_exact_when_every_tile_publishes(nthreads, width):
+    # the bounded wait changes nothing while every predecessor publishes:
+    # numpy's wrapping cumsum, status word 0
+    agg = o.words(77, 20000).astype(np.uint32).view(np.int32)
+    ex, inc, st = o.lookback_bounded(agg, nthreads, width=width)
+    ref = np.cumsum(agg.astype(np.int64)).astype(np.int32)  # wraps like int32
+    assert st == 0
+    assert (inc == ref).all() and ex[0] == 0 and (ex[1:] == ref[:-1]).all()
+
+
+@pytest.mark.parametrize("withhold", [0, 1, 7, 3000, 4095])
+@pytest.mark.parametrize("nthreads", [1, 8])
+def test_bounded_lookback_withheld_predecessor_reports_timeout(withhold, nthreads):
+    """A tile that never publishes: every wait still ends, the status word
+    carries LOOKBACK_TIMEOUT, and the library decodes that word to
+    LCPP_ERR_LOOKBACK_TIMEOUT (-5), as lcpp_temp_status reports a device
+    give-up.  Tiles before the withheld one are exact; tiles after it lost
+    exactly its aggregate (an unpublished word reads as 0)."""
+    import lc_parallel_primitive_amd as lcpp
+
+    n = 4096
+    agg = o.words(78, n).astype(np.uint32).view(np.int32)
+    ex, inc, st = o.lookback_bounded(agg, nthreads, withhold=withhold, spin_limit=2000)
+    ref = np.cumsum(agg.astype(np.int64))
+    last = withhold == n - 1  # no tile waits on the last one
+    assert (st & 1) == (0 if last else 1)
+    assert lcpp.lib().lcpp_device_status_decode(st) == (0 if last else -5)
+    w = withhold
+    assert (inc[:w] == ref[:w].astype(np.int32)).all()
+    lost = (ref[w + 1:] - int(agg[w])).astype(np.int32)
+    assert (inc[w + 1:] == lost).all()
+
+
+
 # ------------------------------------------------------------------ radix sort
 @pytest.mark.parametrize("dt", SORT_DTYPES)
 @pytest.mark.parametrize("nthreads", [1, 4])
