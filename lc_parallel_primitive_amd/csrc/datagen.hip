@@ -218,16 +218,24 @@ __device__ __forceinline__ uint32_t dg_xcd_tile(uint32_t b, uint32_t grid, uint3
     return (g << log_group) + ((r & 7) << log_run) + (r >> 3);
 }
 
+// `zero` is 0 at run time: every stored vector depends on all of the
+// thread's loads, so the tile is held in registers before the first store
+// (as in the scan, whose stores wait for the look-back).
 template <int VECS>
-__global__ __launch_bounds__(256) void shape_scan_tile(const u32x4c *__restrict__ in, u32x4c *__restrict__ out)
+__global__ __launch_bounds__(256) void shape_scan_tile(const u32x4c *__restrict__ in, u32x4c *__restrict__ out,
+                                                       uint32_t zero)
 {
     const uint64_t base = (uint64_t)blockIdx.x * 256 * VECS;
     u32x4c v[VECS];
 #pragma unroll
     for (int k = 0; k < VECS; ++k) v[k] = __builtin_nontemporal_load(in + base + (uint64_t)k * 256 + threadIdx.x);
-    __syncthreads();  // the whole tile is in registers before the first store, as in the scan
+    u32x4c t = v[0];
 #pragma unroll
-    for (int k = 0; k < VECS; ++k) __builtin_nontemporal_store(v[k], out + base + (uint64_t)k * 256 + threadIdx.x);
+    for (int k = 1; k < VECS; ++k) t ^= v[k];
+    const uint32_t dep = (t.x ^ t.y ^ t.z ^ t.w) & zero;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < VECS; ++k) __builtin_nontemporal_store(v[k] + dep, out + base + (uint64_t)k * 256 + threadIdx.x);
 }
 
 __global__ __launch_bounds__(256) void shape_grid_stride(const u32x4c *__restrict__ in, u32x4c *__restrict__ out,
@@ -259,7 +267,7 @@ __device__ __forceinline__ uint32_t shape_pos(int shape, uint32_t tile, uint32_t
 
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6, 6)))
 void shape_onesweep_tile(const uint32_t *__restrict__ in, uint32_t *__restrict__ out, uint32_t n, int shape,
-                         uint32_t log_run)
+                         uint32_t log_run, uint32_t zero)
 {
     const uint32_t tile = dg_xcd_tile(blockIdx.x, gridDim.x, log_run);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -267,11 +275,15 @@ void shape_onesweep_tile(const uint32_t *__restrict__ in, uint32_t *__restrict__
     uint32_t k[32];
 #pragma unroll
     for (int u = 0; u < 32; ++u) k[u] = __builtin_nontemporal_load(in + base + wave * 2048u + (uint32_t)u * 64u + lane);
-    __syncthreads();  // the tile is loaded before it is written, as in the onesweep
+    uint32_t t = 0;  // as in shape_scan_tile: the stores wait for every load
+#pragma unroll
+    for (int u = 0; u < 32; ++u) t ^= k[u];
+    const uint32_t dep = t & zero;
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
         const uint32_t p = shape_pos(shape, tile, (uint32_t)j * 512u + tid, n);
-        if (p < n) out[p] = k[j];
+        if (p < n) out[p] = k[j] + dep;
     }
 }
 
@@ -293,7 +305,7 @@ int lcpp_dg_copy_shape(const void *in, void *out, uint64_t n, int shape, void *s
     if (shape == 0) return lcpp_copy_probe_u32(in, out, n, stream);
     if (shape == 1 || shape == 2) {
         if (n % (256 * 20 * 4)) return -1;
-        shape_scan_tile<20><<<(uint32_t)(n / (256 * 20 * 4)), 256, shape == 1 ? 36u << 10 : 0u, s>>>(vi, vo);
+        shape_scan_tile<20><<<(uint32_t)(n / (256 * 20 * 4)), 256, shape == 1 ? 36u << 10 : 0u, s>>>(vi, vo, 0u);
     } else if (shape == 3) {
         if (n % 4) return -1;
         shape_grid_stride<<<2048, 256, 0, s>>>(vi, vo, n / 4);
@@ -302,7 +314,7 @@ int lcpp_dg_copy_shape(const void *in, void *out, uint64_t n, int shape, void *s
         const uint32_t log_run = shape == 4 || shape == 7 ? 0u : 4u;
         shape_onesweep_tile<<<(uint32_t)(n / 16384), 512, 48u << 10, s>>>(static_cast<const uint32_t *>(in),
                                                                    static_cast<uint32_t *>(out), (uint32_t)n, shape,
-                                                                   log_run);
+                                                                   log_run, 0u);
     } else {
         return -1;
     }
