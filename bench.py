@@ -355,7 +355,7 @@ def main():
                                                  ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(x.data_ptr()),
                                                  ctypes.c_void_p(uk.data_ptr()), ctypes.c_void_p(ag.data_ptr()),
                                                  ctypes.c_void_p(nr.data_ptr()), n, sp), "rbk"),
-                20, "reduce_by_key")
+                20, "reduce_by_key_tile")
             del k, x, uk, ag, t1
         if want("segment"):
             n, S = 1 << 27, 1 << 20

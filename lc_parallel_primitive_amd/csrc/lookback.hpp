@@ -71,7 +71,9 @@ constexpr int kLbPollWidth = 16;
 // the tiles after the nearest INCLUSIVE predecessor, folded onto that
 // predecessor's inclusive value.  Every lane returns it.  `op` must be
 // commutative (sum, min, max): a window is reduced as a tree.
-template <class T, class Op>
+// W = predecessors polled per round trip (kLbPollWidth, or up to 64 where few
+// tiles compete for the memory system, as in ReduceByKey's emit launch).
+template <int W = kLbPollWidth, class T, class Op>
 __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T identity, const WaitCtl &ctl)
 {
     const uint32_t lane = lane_id();
@@ -79,11 +81,12 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
     int64_t top = (int64_t)tile - 1;
     uint32_t spins = 0;
     for (;;) {
-        // Lane l < kLbPollWidth polls predecessor top - l; the other lanes
+        // Lane l < W polls predecessor top - l; the other lanes
         // re-read lane 0's word (same cache line) and are neutral.  The load
         // is unconditional (an index below 0 reads word 0 and is then treated
         // as INCLUSIVE identity), so no branch separates issue and wait.
-        const bool poller = lane < (uint32_t)kLbPollWidth;
+        static_assert(W >= 1 && W <= kWave, "poll width");
+        const bool poller = lane < (uint32_t)W;
         const int64_t j = top - (int64_t)(poller ? lane : 0u);
         const uint64_t jj = j < 0 ? 0 : (uint64_t)j;
         uint32_t s;
@@ -120,7 +123,7 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
         const bool found = incl != 0;
         excl = op(excl, wave_allreduce(acc, op));
         if (found) break;
-        top -= kLbPollWidth;
+        top -= W;
     }
     return excl;
 }
@@ -128,7 +131,7 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
 // Plain scan tile: publish PARTIAL(agg), wait for the prefix, publish
 // INCLUSIVE(prefix op agg).  Returns the exclusive prefix (identity for
 // tile 0) in every lane.
-template <class T, class Op>
+template <int W = kLbPollWidth, class T, class Op>
 __device__ __forceinline__ T lb_scan_tile(uint64_t *words, uint32_t tile, T agg, Op op, T identity,
                                           const WaitCtl &ctl)
 {
@@ -138,7 +141,7 @@ __device__ __forceinline__ T lb_scan_tile(uint64_t *words, uint32_t tile, T agg,
         return identity;
     }
     if (lane == 0) lb_publish(words, tile, agg, kStPartial, ctl);
-    const T excl = lb_wait_prefix(words, tile, op, identity, ctl);
+    const T excl = lb_wait_prefix<W>(words, tile, op, identity, ctl);
     if (lane == 0) lb_publish(words, tile, op(excl, agg), kStInclusive, ctl);
     return excl;
 }
@@ -147,14 +150,14 @@ __device__ __forceinline__ T lb_scan_tile(uint64_t *words, uint32_t tile, T agg,
 // its inclusive value at once (the fold since its last head) and publishes
 // INCLUSIVE(agg) before it waits; it waits only if its first element is not
 // a head (`need_prefix`).  A tile without a head is a plain scan tile.
-template <class T, class Op>
+template <int W = kLbPollWidth, class T, class Op>
 __device__ __forceinline__ T lb_segmented_tile(uint64_t *words, uint32_t tile, T agg, bool has_head,
                                               bool need_prefix, Op op, T identity, const WaitCtl &ctl)
 {
-    if (!has_head) return lb_scan_tile(words, tile, agg, op, identity, ctl);
+    if (!has_head) return lb_scan_tile<W>(words, tile, agg, op, identity, ctl);
     if (lane_id() == 0) lb_publish(words, tile, agg, kStInclusive, ctl);
     if (tile == 0 || !need_prefix) return identity;
-    return lb_wait_prefix(words, tile, op, identity, ctl);
+    return lb_wait_prefix<W>(words, tile, op, identity, ctl);
 }
 
 namespace {

@@ -104,10 +104,22 @@ def test_temp_bytes_queries(L):
     rc, b = _q(L.lcpp_scan_by_key_temp_bytes, 2, 5, 1 << 27)
     assert rc == 0 and b == HDR + (1 << 15) * 16
     # reduce by key: head-count words + open-run words, each 256-byte aligned
+    # reduce by key: look-back words per group of 64 tiles (count, fold),
+    # per-tile summaries (count word, fold), dense run slots (128 (key, value)
+    # entries per tile), then the overflow staging area, one (key, value)
+    # entry per element of every tile; each part 256-byte aligned
+    def rbk(kb, vb, n, tile):
+        tiles = -(-n // tile)
+        groups = -(-tiles // 64)
+        up = lambda x: -(-x // 256) * 256
+        return (HDR + up(tiles * 4) + up(tiles * vb) + up(groups * 8) + up(groups * 8 * (1 if vb == 4 else 2))
+                + up(tiles * 128 * kb) + up(tiles * 128 * vb) + up(tiles * tile * kb) + up(tiles * tile * vb))
     rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 0, 0, 1 << 28)
-    assert rc == 0 and b == HDR + 2 * (1 << 15) * 8
+    assert rc == 0 and b == rbk(4, 4, 1 << 28, 8192)
     rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 5, 5, 100)
-    assert rc == 0 and b == HDR + 256 + 256
+    assert rc == 0 and b == rbk(8, 8, 100, 4096)
+    rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 3, 2, 300_000)
+    assert rc == 0 and b == rbk(8, 4, 300_000, 8192)
     assert _q(L.lcpp_reduce_by_key_temp_bytes, 0, 9, 100)[0] == -3
     # segment reduce needs none (as the reference)
     assert _q(L.lcpp_segment_reduce_temp_bytes, 2, 1 << 20) == (0, 0)

@@ -203,6 +203,30 @@ def test_reduce_by_key_sizes_ops_guard(gpu, n, op):
     assert (uk[r:] == 0).all() and (ag[r:] == 0).all(), "write past the last run"
 
 
+@pytest.mark.parametrize("vdt", [np.int32, np.float64])
+@pytest.mark.parametrize("op", ["sum", "min", "max"])
+def test_reduce_by_key_across_emit_groups(gpu, vdt, op):
+    """Run counts and folds carried across the emit launch's groups of 64
+    tiles: dense runs (every tile's staging area nearly full), runs longer
+    than a group (whole groups without a head), and one run over everything."""
+    tile = 8192 if np.dtype(vdt).itemsize == 4 else 4096
+    n = 3 * 64 * tile + 4097
+    for mean in (1.5, 1.5 * 64 * tile, float(n) * 10):
+        keys = run_keys(n, mean, 8, np.int64)
+        v = values(vdt, n, 9)
+        log(f"ReduceByKey groups n={n} mean={mean:.0f} {np.dtype(vdt).name} {op}")
+        uk, ag, r = reduce_by_key(keys, v, op, guard=8)
+        ek, ea = o.reduce_by_key(keys, v, OPS[op])
+        assert r == ek.size
+        assert (uk[:r] == ek).all()
+        if np.dtype(vdt).kind == "f" and op == "sum":
+            s_, ab = o.reduce_by_key_f64(keys, v)
+            assert (np.abs(ag[:r] - s_) <= RTOL * ab + 1e-30).all()
+        else:
+            assert (ag[:r] == ea).all()
+        assert (uk[r:] == 0).all() and (ag[r:] == 0).all(), "write past the last run"
+
+
 def test_reduce_by_key_empty_and_single(gpu):
     uk, ag, r = reduce_by_key(np.empty(0, np.int32), np.empty(0, np.int32))
     assert r == 0

@@ -125,9 +125,15 @@ def test_by_key_withheld_tile_reports_timeout(gpu):
     assert status(t) == OK
     assert (g.to_host(out) == o.scan_by_key(keys, vals, inclusive=True)).all()
 
+    # ReduceByKey's look-back runs over groups of 64 tiles (its emit launch):
+    # withhold group 4 of 7
+    n = 7 * 64 * 8192 - 1000
+    keys = (np.arange(n) // 97).astype(np.int32)
+    vals = g.random_array(np.int32, n, seed=5)
+    dk, dv = g.to_dev(keys), g.to_dev(vals)
     uk, agg, runs = g.empty(n, np.int32), g.empty(n, np.int32), g.empty(1, np.uint32)
     t = _temp(L.lcpp_reduce_by_key_temp_bytes, 0, 0, n)
-    log("status: reduce by key tile 4 withheld")
+    log("status: reduce by key group 4 withheld")
     with withheld(4):
         assert L.lcpp_reduce_by_key(0, 0, 0, _p(t), t.numel(), _p(dk), _p(dv), _p(uk), _p(agg), _p(runs), n,
                                     _sp()) == 0
