@@ -208,10 +208,9 @@ int lcpp_scan_inclusive_sum_by_key(lcpp_dtype k, lcpp_dtype v, void *temp, size_
                                    const void *keys_in, const void *vals_in, void *vals_out,
                                    uint64_t n, void *stream);
 /* replaces DeviceReduce::GetReduceByKeyTempStorageBytes<K,V>(num_elements), device_reduce.h:110-125.
- * Unlike the reference's O(tiles) state, the temp holds a run staging area of about
- * n * (sizeof K + sizeof V) bytes (plus 1/64 of that for dense slots): the pass over the
- * data stages each tile's runs instead of waiting for the run count before the tile, and a
- * second launch moves them.  Only entries of actual runs are written.  n < 2^32. */
+ * Besides the reference's O(tiles) look-back state, the temp holds a run staging area of
+ * about n * (sizeof K + sizeof V) / 64 bytes: tiles with at most 128 runs stage them instead
+ * of waiting for the run count before the tile, and a second launch moves them.  n < 2^32. */
 int lcpp_reduce_by_key_temp_bytes(lcpp_dtype k, lcpp_dtype v, uint64_t n, size_t *bytes);
 /* replaces DeviceReduce::ReduceByKey(cmdlist, temp, d_keys_in, d_values_in, d_unique_out,
  * g_aggregates_out, g_num_runs_out, reduce_op, num_elements), device_reduce.h:277-318:

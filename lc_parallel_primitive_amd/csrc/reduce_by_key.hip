@@ -7,57 +7,57 @@
 // compared in their own type); unique_out[r] = its key, aggregates_out[r] =
 // the op-fold of its values, *num_runs_out = the number of runs.
 //
-// Design (tile machinery in by_key.hpp): two launches, and no wait in the
-// pass over the data.
+// Design (tile machinery in by_key.hpp): the pass over the data waits only
+// in tiles with many runs.
 //  * rbk_tile: one 256-thread workgroup per tile of 8192 4-byte values
 //    (4096 8-byte).  It finds the tile's segment heads and folds its runs with
 //    tile-local prefixes (reduce-then-rescan, by_key.hpp; the prefixes of the
-//    32 (vector, wave) slices are scanned once per tile by wave 0).  Entry i
-//    of the tile is the run closed by its i-th head: that run's key and its
-//    fold over this tile's elements (entry 0 lacks the part of its run in
-//    earlier tiles).  The first 128 entries are gathered in LDS and stored
-//    contiguously into the tile's slot of a dense staging area (runs of mean
-//    128 give 64 per tile); further ones go to the tile's entries of a sparse
-//    overflow area.  It also writes the tile's summary: its head count,
-//    whether it has a head, and the fold since its last head (or of the whole
-//    tile).  Tile 0 zeroes the status word and the emit launch's look-back
-//    words (this launch reads none of them).
-//    The reference's single pass (reduce_by_key.h:90-258) waits on two
-//    decoupled look-backs per tile instead: the run count before the tile (a
-//    plain scan) and the fold of the run entering it (a segmented scan).  On
-//    this part those waits cost ~130 of ~500 us at 2^28 (int32 keys, f32
-//    values, runs of mean 128): a tile here carries only 64 KiB against the
-//    scan's 160 KiB, so a wait of a few microseconds is a large share of its
-//    life.
+//    32 (vector, wave) slices are scanned once per tile by wave 0), writes the
+//    tile's summary (its head count, whether it has a head, the fold since its
+//    last head or of the whole tile) and publishes the same as decoupled
+//    look-back words (the count as PARTIAL; the fold as INCLUSIVE when the
+//    tile has a head, else PARTIAL).
+//    - A tile with at most 128 heads does not wait: entry i = the run closed
+//      by its i-th head (that run's key and its fold over this tile's
+//      elements; entry 0 lacks the part of its run in earlier tiles) is
+//      gathered in LDS and stored contiguously into the tile's slot of a
+//      dense staging area.  Runs of mean 128 give 64 per tile.
+//    - A tile with more heads waits for the run count before it (walking
+//      back to the nearest tile that published an inclusive count) and the
+//      fold entering it (to the nearest tile with a head), publishes its
+//      inclusive count and writes its runs to the outputs directly.
+//    The reference's single pass (reduce_by_key.h:90-258) waits on both
+//    look-backs in every tile.  On this part those waits cost ~130 of ~500
+//    us at 2^28 (int32 keys, f32 values, runs of mean 128): a tile here
+//    carries only 64 KiB against the scan's 160 KiB, so a wait of a few
+//    microseconds is a large share of its life.
 //  * rbk_emit: one workgroup per 64 tiles.  Wave 0 scans their head counts;
 //    the group's prefix is the sum of the counts every earlier group
 //    publishes at its start (read 512 groups per round trip, no chain of
 //    inclusive prefixes).  Wave 1 scans their segmented folds and takes the
 //    fold entering the group from a decoupled look-back over groups (it stops
-//    at the nearest group with a head).  Then the staged runs move to their
-//    final positions, entry 0 of each tile completed with the fold entering
-//    the tile, and the last group writes the last run and the run count (the
+//    at the nearest group with a head).  Staged runs move to their final
+//    positions, entry 0 of each tile completed with the fold entering the
+//    tile.  The last group writes the last run and the run count (the
 //    reference writes them from its last tile, reduce_by_key.h:231-254).
-// Bytes: keys + values read once, plus (sizeof K + sizeof V) per run
-// written, staged and moved (16 MB each way at 2^28, runs of 128).  Temp:
-// the dense slots (128 entries per tile) and the overflow area (one entry per
-// element, since every element may start a run; only entries of tiles with
-// more than 128 runs are touched).
+// Bytes: keys + values read once, plus (sizeof K + sizeof V) per run written
+// (runs of tiles with at most 128 heads twice, and read once).  Temp: O(n /
+// 64) for the dense slots, plus per-tile summaries and look-back words.
 #include "by_key.hpp"
 
 namespace lcpp {
 namespace {
 
-constexpr uint32_t kRbkGroup = 64;     // tiles per rbk_emit workgroup (one wave's lanes)
-// Runs per tile gathered in LDS and stored contiguously into the tile's slot
-// of the dense staging area (runs of mean 128 give 64 per tile); a tile's
-// further runs go to its entries of the sparse overflow area.
-constexpr uint32_t kRbkSlot = 128;
+constexpr uint32_t kRbkGroup = 64;  // tiles per rbk_emit workgroup (one wave's lanes)
+constexpr uint32_t kRbkSlot = 128;  // runs a tile may stage (its dense slot)
+constexpr uint32_t kRbkHeadBit = 0x80000000u;   // summary count word: the tile has a head
+constexpr uint32_t kRbkDenseBit = 0x40000000u;  // summary count word: more than kRbkSlot heads
+constexpr uint32_t kRbkCountMask = 0x3FFFFFFFu;
 
 template <class K, class V>
 struct RbkLayout {
-    uint64_t tiles, groups, count_off, fold_off, cwords_off, vwords_off, pkeys_off, pvals_off, skeys_off, svals_off,
-        total;
+    uint64_t tiles, groups, cwords_off, vwords_off, tcwords_off, tvwords_off, count_off, fold_off, pkeys_off,
+        pvals_off, total;
 };
 template <class K, class V>
 RbkLayout<K, V> rbk_layout(uint64_t n)
@@ -65,49 +65,55 @@ RbkLayout<K, V> rbk_layout(uint64_t n)
     RbkLayout<K, V> L{};
     L.tiles = bk_tiles<V>(n);
     L.groups = ceil_div(L.tiles, kRbkGroup);
-    // [status header | group look-back words (zeroed by tile 0) | tile
-    //  summaries | dense staging slots | overflow staging]
+    // [status header | group look-back words | tile look-back words (all
+    //  zeroed by one fill) | tile summaries | dense slots]
     L.cwords_off = kStatusBytes;
     L.vwords_off = L.cwords_off + align_up(L.groups * 8, 256);
-    L.count_off = L.vwords_off + align_up(L.groups * 8 * lb_words<V>(), 256);
+    L.tcwords_off = L.vwords_off + align_up(L.groups * 8 * lb_words<V>(), 256);
+    L.tvwords_off = L.tcwords_off + align_up(L.tiles * 8, 256);
+    L.count_off = L.tvwords_off + align_up(L.tiles * 8 * lb_words<V>(), 256);
     L.fold_off = L.count_off + align_up(L.tiles * 4, 256);
     L.pkeys_off = L.fold_off + align_up(L.tiles * sizeof(V), 256);
     L.pvals_off = L.pkeys_off + align_up(L.tiles * kRbkSlot * sizeof(K), 256);
-    L.skeys_off = L.pvals_off + align_up(L.tiles * kRbkSlot * sizeof(V), 256);
-    L.svals_off = L.skeys_off + align_up(L.tiles * bk_tile<V>() * sizeof(K), 256);
-    L.total = L.svals_off + align_up(L.tiles * bk_tile<V>() * sizeof(V), 256);
+    L.total = L.pvals_off + align_up(L.tiles * kRbkSlot * sizeof(V), 256);
     return L;
 }
 
 __global__ void rbk_zero_runs(uint32_t *num_runs) { *num_runs = 0; }
 
-constexpr uint32_t kRbkHeadBit = 0x80000000u;  // summary count word: has a head
+// LDS of one tile.  Keys sit in LDS when they fit in 32 KiB: the registers
+// that held them are free for pass 2 (150 -> ~100 VGPRs).
+template <class K, class V>
+struct RbkSmem {
+    static constexpr bool kKeysInLds = bk_tile<V>() * sizeof(K) <= 32768;
+    K keys[kKeysInLds ? bk_tile<V>() : 1];
+    K last[kBkVecs][kBkWaves];
+    K pred;
+    V S[kBkVecs][kBkWaves];
+    uint32_t C[kBkVecs][kBkWaves];
+    uint32_t F[kBkVecs];
+    K stk[kRbkSlot];
+    V stv[kRbkSlot];
+    V pw[kBkVecs * kBkWaves];
+    uint32_t cw[kBkVecs * kBkWaves];
+    uint32_t pf;  // bit l: a head before slice l
+    uint32_t tc;
+};
 
 template <class K, class V, class Op>
 __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict__ keys, const V *__restrict__ vin,
                                                             uint32_t n, uint32_t *__restrict__ tile_count,
                                                             V *__restrict__ tile_fold, K *__restrict__ pkeys,
-                                                            V *__restrict__ pvals, K *__restrict__ skeys,
-                                                            V *__restrict__ svals, int vec_ok,
-                                                            uint64_t *__restrict__ zero_words, uint32_t zero_count)
+                                                            V *__restrict__ pvals, K *__restrict__ unique_out,
+                                                            V *__restrict__ agg_out, uint64_t *tcwords,
+                                                            uint64_t *tvwords, int vec_ok, WaitCtl ctl)
 {
     constexpr int VP = bk_vp<V>();
     constexpr uint32_t TILE = bk_tile<V>();
-    // keys of the tile in LDS when they fit in 32 KiB: the registers that
-    // held them are free for pass 2 (150 -> ~100 VGPRs)
-    constexpr bool kKeysInLds = TILE * sizeof(K) <= 32768;
-    __shared__ K s_keys[kKeysInLds ? TILE : 1];
-    __shared__ K s_last[kBkVecs][kBkWaves];
-    __shared__ K s_pred;
-    __shared__ V s_S[kBkVecs][kBkWaves];
-    __shared__ uint32_t s_C[kBkVecs][kBkWaves];
-    __shared__ uint32_t s_F[kBkVecs];
-    __shared__ K s_stk[kRbkSlot];
-    __shared__ V s_stv[kRbkSlot];
-    __shared__ V s_pw[kBkVecs * kBkWaves];
-    __shared__ uint32_t s_cw[kBkVecs * kBkWaves];
-    __shared__ uint32_t s_tc;
-
+    constexpr bool kKeysInLds = RbkSmem<K, V>::kKeysInLds;
+    __shared__ RbkSmem<K, V> sm;
+    __shared__ uint32_t s_cpre;
+    __shared__ V s_vpre;
     Op op;
     const V ident = op_identity<Op, V>();
     const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
@@ -118,13 +124,9 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
 
     BkRegs<K, V> r;
     bk_load<true>(r, keys, vin, base, valid, fast, tid);
-    // the call's status word and the emit launch's look-back words start at
-    // zero (this launch reads none of them: no separate fill launch)
-    if (tile == 0)
-        for (uint32_t i = tid; i < zero_count; i += kBkBlock) zero_words[i] = 0;
-    if (tid < kBkVecs) s_F[tid] = 0;
+    if (tid < kBkVecs) sm.F[tid] = 0;
     K prev0[kBkVecs];
-    uint32_t fl = bk_heads<K, VP>(r.key, prev0, s_last, s_pred, keys, base, tile, tid);
+    uint32_t fl = bk_heads<K, VP>(r.key, prev0, sm.last, sm.pred, keys, base, tile, tid);
     if (valid != TILE) {
         // a ragged last tile: items past n are neither heads nor folded
 #pragma unroll
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
 #pragma unroll
         for (int k = 0; k < kBkVecs; ++k)
 #pragma unroll
-            for (int j = 0; j < VP; ++j) s_keys[bk_elem<V>(k, tid, j)] = r.key[k][j];
+            for (int j = 0; j < VP; ++j) sm.keys[bk_elem<V>(k, tid, j)] = r.key[k][j];
     }
 
     // head counts: per vector a wave scan, wave totals to LDS
@@ -150,7 +152,7 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
         const uint32_t c = (uint32_t)__builtin_popcount((fl >> (k * VP)) & ((1u << VP) - 1u));
         const uint32_t ci = wave_inclusive_scan(c, SumOp());
         exC[k] = ci - c;
-        if (lane == kWave - 1) s_C[k][wave] = ci;
+        if (lane == kWave - 1) sm.C[k][wave] = ci;
     }
 
     // pass 1: per vector, (has-head, open fold) pairs, their wave scan, wave
@@ -170,67 +172,96 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
         exS[k] = lane == 0 ? ident : su;
         exF |= (uint32_t)(lane != 0 && fu) << k;
         if (lane == kWave - 1) {
-            s_S[k][wave] = s;
-            if (f) atomicOr(&s_F[k], 1u << wave);
+            sm.S[k][wave] = s;
+            if (f) atomicOr(&sm.F[k], 1u << wave);
         }
     }
     __syncthreads();
 
     // wave 0: the exclusive prefixes of the (vector, wave) slices in tile
-    // order (lane k * 4 + w: its fold since the tile's last earlier head and
-    // its head count), once per tile instead of a serial loop in every
-    // thread; their inclusive totals are the tile's summary
-    static_assert(kBkVecs * kBkWaves <= kWave, "one lane per slice");
+    // order (lane k * 4 + w: its fold since the tile's last earlier head, a
+    // head before it, its head count), once per tile instead of a serial loop
+    // in every thread; their inclusive totals are the tile's summary, also
+    // published as look-back words
+    static_assert(kBkVecs * kBkWaves <= 32, "one lane and one pf bit per slice");
     constexpr uint32_t kSlices = kBkVecs * kBkWaves;
     if (wave == 0) {
         const bool in = lane < kSlices;
-        const uint32_t sk_ = in ? lane / kBkWaves : 0, sw = in ? lane % kBkWaves : 0;
-        bool f = in && ((s_F[sk_] >> sw) & 1u) != 0;
-        V v = in ? s_S[sk_][sw] : ident;
-        const uint32_t c = in ? s_C[sk_][sw] : 0u;
+        const uint32_t k_ = in ? lane / kBkWaves : 0, w_ = in ? lane % kBkWaves : 0;
+        bool f = in && ((sm.F[k_] >> w_) & 1u) != 0;
+        V v = in ? sm.S[k_][w_] : ident;
+        const uint32_t c = in ? sm.C[k_][w_] : 0u;
         wave_seg_scan(f, v, op);
         const uint32_t ci = wave_inclusive_scan(c, SumOp());
         const V vu = shfl_up(v, 1);
+        const uint64_t heads_incl = ballot(f);
         if (in) {
-            s_pw[lane] = lane == 0 ? ident : vu;
-            s_cw[lane] = ci - c;
+            sm.pw[lane] = lane == 0 ? ident : vu;
+            sm.cw[lane] = ci - c;
         }
-        const bool tf = read_lane((int)f, kSlices - 1) != 0;
-        const V ts = read_lane(v, kSlices - 1);
         const uint32_t tc = read_lane(ci, kSlices - 1);
+        const V ts = read_lane(v, kSlices - 1);
+        const bool tf = ((heads_incl >> (kSlices - 1)) & 1u) != 0;
         if (lane == 0) {
-            tile_count[tile] = tc | (tf ? kRbkHeadBit : 0u);
+            sm.pf = (uint32_t)(heads_incl << 1);  // a head in slices < l
+            sm.tc = tc;
+            tile_count[tile] = tc | (tf ? kRbkHeadBit : 0u) | (tc > kRbkSlot ? kRbkDenseBit : 0u);
             tile_fold[tile] = ts;
-            s_tc = tc;
+            lb_publish(tcwords, tile, tc, tile == 0 ? kStInclusive : kStPartial, ctl);
+            lb_publish(tvwords, tile, ts, tile == 0 || tf ? kStInclusive : kStPartial, ctl);
         }
     }
     __syncthreads();
 
-    // pass 2: rescan from the tile-local prefixes; the i-th head of the tile
-    // closes staged entry i (the run before it)
-    K *const sk = skeys + (uint64_t)tile * TILE;
-    V *const sv = svals + (uint64_t)tile * TILE;
+    // more than kRbkSlot heads: wait for the run count before the tile (wave
+    // 0) and the fold entering it (wave 1), then write the runs directly
+    const bool direct = sm.tc > kRbkSlot;
+    if (direct) {
+        if (wave == 0) {
+            uint32_t p = 0;
+            if (tile > 0) {
+                p = lb_wait_prefix(tcwords, tile, SumOp(), 0u, ctl);
+                if (lane == 0) lb_publish(tcwords, tile, p + sm.tc, kStInclusive, ctl);
+            }
+            if (lane == 0) s_cpre = p;
+        } else if (wave == 1) {
+            const V p = tile > 0 ? lb_wait_prefix(tvwords, tile, op, ident, ctl) : ident;
+            if (lane == 0) s_vpre = p;
+        }
+        __syncthreads();
+    }
+    const uint32_t cpre = direct ? s_cpre : 0u;
+    const V vpre = direct ? s_vpre : ident;
+
+    // pass 2: rescan from the slice prefixes; a head closes the run before it
+    const uint32_t pf = sm.pf;
 #pragma unroll
     for (int k = 0; k < kBkVecs; ++k) {
-        const V pw = s_pw[k * kBkWaves + wave];
+        const uint32_t sl = k * kBkWaves + wave;
+        const V pw0 = sm.pw[sl];
+        const V pw = ((pf >> sl) & 1u) ? pw0 : op(vpre, pw0);
         V s = ((exF >> k) & 1u) ? exS[k] : op(pw, exS[k]);
-        uint32_t c = s_cw[k * kBkWaves + wave] + exC[k];
+        // staged: the tile's heads before this item (its entry index);
+        // direct: all heads before it (it closes run c - 1)
+        uint32_t c = cpre + sm.cw[sl] + exC[k];
 #pragma unroll
         for (int j = 0; j < VP; ++j) {
             const uint32_t e = bk_elem<V>(k, tid, j);
             if ((fl >> (k * VP + j)) & 1u) {
                 K key;
-                if constexpr (kKeysInLds) key = e > 0 ? s_keys[e - 1] : s_pred;
+                if constexpr (kKeysInLds) key = e > 0 ? sm.keys[e - 1] : sm.pred;
                 else key = j > 0 ? r.key[k][j - 1] : prev0[k];
-                // the first kRbkSlot entries are gathered in LDS and stored
-                // contiguously below; c < the tile's head count <= TILE
-                // keeps the rest inside the tile's overflow entries
-                if (c < kRbkSlot) {
-                    s_stk[c] = key;
-                    s_stv[c] = s;
+                if (direct) {
+                    // c - 1 < n by construction; the bound keeps a broken
+                    // invariant (a wait past its spin limit) from writing
+                    // outside the outputs
+                    if (c > 0 && c - 1 < n) {
+                        unique_out[c - 1] = key;
+                        agg_out[c - 1] = s;
+                    }
                 } else {
-                    sk[c] = key;
-                    sv[c] = s;
+                    sm.stk[c] = key;  // c < the tile's head count <= kRbkSlot
+                    sm.stv[c] = s;
                 }
                 ++c;
                 s = r.val[k][j];
@@ -239,11 +270,12 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
             }
         }
     }
-    __syncthreads();
-    const uint32_t m = s_tc < kRbkSlot ? s_tc : kRbkSlot;
-    for (uint32_t i = tid; i < m; i += kBkBlock) {
-        pkeys[(uint64_t)tile * kRbkSlot + i] = s_stk[i];
-        pvals[(uint64_t)tile * kRbkSlot + i] = s_stv[i];
+    if (!direct) {
+        __syncthreads();
+        for (uint32_t i = tid; i < sm.tc; i += kBkBlock) {
+            pkeys[(uint64_t)tile * kRbkSlot + i] = sm.stk[i];
+            pvals[(uint64_t)tile * kRbkSlot + i] = sm.stv[i];
+        }
     }
 }
 
@@ -294,12 +326,10 @@ __global__ __launch_bounds__(kBkBlock) void rbk_emit_kernel(const K *__restrict_
                                                             const uint32_t *__restrict__ tile_count,
                                                             const V *__restrict__ tile_fold,
                                                             const K *__restrict__ pkeys, const V *__restrict__ pvals,
-                                                            const K *__restrict__ skeys, const V *__restrict__ svals,
                                                             K *__restrict__ unique_out, V *__restrict__ agg_out,
                                                             uint32_t *__restrict__ num_runs, uint64_t *cwords,
                                                             uint64_t *vwords, WaitCtl ctl)
 {
-    constexpr uint32_t TILE = bk_tile<V>();
     __shared__ uint32_t s_cnt[kRbkGroup], s_base[kRbkGroup];
     __shared__ V s_vpre[kRbkGroup];
     __shared__ uint32_t s_gcount;
@@ -313,32 +343,32 @@ __global__ __launch_bounds__(kBkBlock) void rbk_emit_kernel(const K *__restrict_
     const uint32_t ng = tiles - t0 < kRbkGroup ? tiles - t0 : kRbkGroup;
 
     // waves 0 and 1: the group's summaries, one tile per lane; wave 0 scans
-    // the head counts and runs their look-back over groups, wave 1 the
-    // segmented folds
+    // the head counts, wave 1 the segmented folds
     if (wave < 2) {
         const bool in = lane < ng;
-        const uint32_t cw = in ? tile_count[t0 + lane] : 0u;
-        const uint32_t cnt = cw & ~kRbkHeadBit;
+        const uint32_t cwd = in ? tile_count[t0 + lane] : 0u;
+        const uint32_t cnt = cwd & kRbkCountMask;
         if (wave == 0) {
             const uint32_t ci = wave_inclusive_scan(cnt, SumOp());
             const uint32_t total = read_lane(ci, kWave - 1);
             if (lane == 0) lb_publish(cwords, g, total, kStPartial, ctl);
             const uint32_t pre = rbk_sum_before(cwords, g, ctl);
-            s_cnt[lane] = cnt;
+            // tiles with more than kRbkSlot heads wrote their runs themselves
+            s_cnt[lane] = (cwd & kRbkDenseBit) ? 0u : cnt;  // staged entries to move
             s_base[lane] = pre + ci - cnt;
             if (lane == 0) s_gcount = pre + total;
         } else {
-            bool f = in && (cw & kRbkHeadBit) != 0;
+            bool f = in && (cwd & kRbkHeadBit) != 0;
             V v = in ? tile_fold[t0 + lane] : ident;
             wave_seg_scan(f, v, op);
             const bool gf = read_lane((int)f, kWave - 1) != 0;
             const V gv = read_lane(v, kWave - 1);
+            // 64 groups polled per round trip: few workgroups compete here
             const V pre = lb_segmented_tile<kWave>(vwords, g, gv, gf, true, op, ident, ctl);
             // exclusive segmented fold entering tile t0 + lane
             const int fu = __shfl_up((int)f, 1);
             const V vu = shfl_up(v, 1);
-            const V ex = lane == 0 ? pre : (fu ? vu : op(pre, vu));
-            s_vpre[lane] = ex;
+            s_vpre[lane] = lane == 0 ? pre : (fu ? vu : op(pre, vu));
             if (lane == kWave - 1) s_gfold = gf ? gv : op(pre, gv);
         }
     }
@@ -365,30 +395,23 @@ __global__ __launch_bounds__(kBkBlock) void rbk_emit_kernel(const K *__restrict_
             }
         }
     }
-    auto emit = [&](uint32_t l, uint32_t i, K key, V v) {
-        const uint32_t idx = s_base[l] + i;  // the i-th head of tile t0 + l closes run idx - 1
-        if (i == 0) v = op(s_vpre[l], v);
-        // idx <= n by construction; the bound keeps a broken invariant (a
-        // look-back wait past its spin limit) from writing outside
-        if (idx > 0 && idx <= n) {
-            unique_out[idx - 1] = key;
-            agg_out[idx - 1] = v;
-        }
-    };
 #pragma unroll
     for (uint32_t u = 0; u < kPerWave; ++u) {
         const uint32_t l = wave + u * kBkWaves;
 #pragma unroll
         for (uint32_t h = 0; h < kSlotLoads; ++h) {
             const uint32_t i = lane + h * kWave;
-            if (l < ng && i < s_cnt[l]) emit(l, i, mk[u][h], mv[u][h]);
+            if (l < ng && i < s_cnt[l]) {
+                const uint32_t idx = s_base[l] + i;  // the i-th head of tile t0 + l closes run idx - 1
+                const V v = i == 0 ? op(s_vpre[l], mv[u][h]) : mv[u][h];
+                // idx <= n by construction; the bound keeps a broken
+                // invariant (a wait past its spin limit) from writing outside
+                if (idx > 0 && idx <= n) {
+                    unique_out[idx - 1] = mk[u][h];
+                    agg_out[idx - 1] = v;
+                }
+            }
         }
-    }
-    // tiles with more than kRbkSlot runs: the rest from their overflow entries
-    for (uint32_t l = wave; l < ng; l += kBkWaves) {
-        const uint32_t cnt = s_cnt[l];
-        const uint64_t src = (uint64_t)(t0 + l) * TILE;
-        for (uint32_t i = kRbkSlot + lane; i < cnt; i += kWave) emit(l, i, skeys[src + i], svals[src + i]);
     }
     // the last run (open at element n - 1) and the run count
     if (g == gridDim.x - 1 && tid == 0) {
@@ -425,21 +448,24 @@ int rbk_launch(void *temp, size_t tb, const void *keys_, const void *in_, void *
     V *tile_fold = reinterpret_cast<V *>(t + L.fold_off);
     uint64_t *cwords = reinterpret_cast<uint64_t *>(t + L.cwords_off);
     uint64_t *vwords = reinterpret_cast<uint64_t *>(t + L.vwords_off);
+    uint64_t *tcwords = reinterpret_cast<uint64_t *>(t + L.tcwords_off);
+    uint64_t *tvwords = reinterpret_cast<uint64_t *>(t + L.tvwords_off);
     K *pkeys = reinterpret_cast<K *>(t + L.pkeys_off);
     V *pvals = reinterpret_cast<V *>(t + L.pvals_off);
-    K *skeys = reinterpret_cast<K *>(t + L.skeys_off);
-    V *svals = reinterpret_cast<V *>(t + L.svals_off);
+    // the status header and both sets of look-back words are contiguous up
+    // to alignment padding: one fill
+    if (lb_init(reinterpret_cast<uint64_t *>(t), L.count_off / 8, s, "reduce_by_key_init") != LCPP_OK)
+        return LCPP_ERR_HIP;
     const WaitCtl ctl = wait_ctl(reinterpret_cast<uint32_t *>(t));
     const int vec_ok = ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(in)) & 15) == 0;
     LCPP_LAUNCH("reduce_by_key_tile", s,
                 (rbk_tile_kernel<K, V, Op><<<(uint32_t)L.tiles, kBkBlock, 0, s>>>(
-                    keys, in, (uint32_t)n, tile_count, tile_fold, pkeys, pvals, skeys, svals, vec_ok,
-                    reinterpret_cast<uint64_t *>(t), (uint32_t)(L.count_off / 8))));
+                    keys, in, (uint32_t)n, tile_count, tile_fold, pkeys, pvals, uk, agg, tcwords, tvwords, vec_ok,
+                    ctl)));
     LCPP_CHECK_LAUNCH();
     LCPP_LAUNCH("reduce_by_key_emit", s,
                 (rbk_emit_kernel<K, V, Op><<<(uint32_t)L.groups, kBkBlock, 0, s>>>(
-                    keys, (uint32_t)n, (uint32_t)L.tiles, tile_count, tile_fold, pkeys, pvals, skeys, svals, uk, agg,
-                    num_runs,
+                    keys, (uint32_t)n, (uint32_t)L.tiles, tile_count, tile_fold, pkeys, pvals, uk, agg, num_runs,
                     cwords, vwords, ctl)));
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;

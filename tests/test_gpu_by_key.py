@@ -227,6 +227,34 @@ def test_reduce_by_key_across_emit_groups(gpu, vdt, op):
         assert (uk[r:] == 0).all() and (ag[r:] == 0).all(), "write past the last run"
 
 
+@pytest.mark.parametrize("op", ["sum", "max"])
+def test_reduce_by_key_dense_and_sparse_tiles_mixed(gpu, op):
+    """Tiles with more than 128 runs (processed again from the input with
+    their prefixes) next to tiles that stage their runs: alternating regions
+    of runs of mean 2 and mean 500, a single dense tile, and a tile with
+    exactly 128 and 129 runs."""
+    n = 40 * 8192 + 77
+    rng = np.random.default_rng(11)
+    mean = np.full(n, 500.0)
+    mean[3 * 8192:9 * 8192] = 2.0        # dense tiles, crossing emit groups? (64-tile groups: no)
+    mean[20 * 8192:21 * 8192] = 1.0      # one all-distinct tile
+    mean[30 * 8192 + 100:31 * 8192] = 3.0
+    heads = rng.random(n) < 1.0 / mean
+    heads[0] = True
+    # tile 12 with exactly 128 heads, tile 13 with 129
+    for t, h in ((12, 128), (13, 129)):
+        heads[t * 8192:(t + 1) * 8192] = False
+        heads[t * 8192 + rng.choice(8192, h, replace=False)] = True
+    keys = (np.cumsum(heads) * 3 % 65_521).astype(np.int32)
+    v = values(np.int32, n, 12)
+    log(f"ReduceByKey mixed dense/sparse tiles {op}")
+    uk, ag, r = reduce_by_key(keys, v, op, guard=8)
+    ek, ea = o.reduce_by_key(keys, v, OPS[op])
+    assert r == ek.size
+    assert (uk[:r] == ek).all() and (ag[:r] == ea).all()
+    assert (uk[r:] == 0).all() and (ag[r:] == 0).all()
+
+
 def test_reduce_by_key_empty_and_single(gpu):
     uk, ag, r = reduce_by_key(np.empty(0, np.int32), np.empty(0, np.int32))
     assert r == 0
