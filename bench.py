@@ -369,7 +369,22 @@ def main():
                                                       ctypes.c_void_p(y.data_ptr()), S, ctypes.c_void_p(db.data_ptr()),
                                                       ctypes.c_void_p(de.data_ptr()), sp), "segment"), 20,
                 "segment_reduce", cpu=lambda: cpu_segment(n, S, b, e))
-            del x, y, db, de
+            idx = torch.empty(S, dtype=torch.int32, device="cuda")
+            add("DeviceSegmentReduce::ArgMin float32 N=2^27 S=2^20", 4 * n + 16 * S,
+                lambda: chk(L.lcpp_segment_reduce_argmin(F32, None, 0, ctypes.c_void_p(x.data_ptr()),
+                                                         ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
+                                                         S, ctypes.c_void_p(db.data_ptr()),
+                                                         ctypes.c_void_p(de.data_ptr()), sp), "segment"), 20,
+                "segment_reduce")
+            # the same segments in a random order: every wave gathers
+            perm = torch.randperm(S, generator=torch.Generator().manual_seed(3)).numpy()
+            pb, pe = torch.from_numpy(b[perm].copy()).cuda(), torch.from_numpy(e[perm].copy()).cuda()
+            add("DeviceSegmentReduce::Sum float32 N=2^27 S=2^20, segments in a random order", 4 * n + 12 * S,
+                lambda: chk(L.lcpp_segment_reduce_sum(F32, None, 0, ctypes.c_void_p(x.data_ptr()),
+                                                      ctypes.c_void_p(y.data_ptr()), S, ctypes.c_void_p(pb.data_ptr()),
+                                                      ctypes.c_void_p(pe.data_ptr()), sp), "segment"), 20,
+                "segment_reduce")
+            del x, y, db, de, idx, perm, pb, pe
         del flush_buf
         result["secondary"] = sec
 

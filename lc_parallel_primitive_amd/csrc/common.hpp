@@ -309,6 +309,19 @@ __device__ __forceinline__ T buf_ld_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff
         return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
     }
 }
+// The same with the streaming (nt) policy.
+template <class T>
+__device__ __forceinline__ T buf_ld_elem_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, kPolicyNT));
+    } else {
+        static_assert(sizeof(T) == 8, "4- or 8-byte types only");
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, 0, kPolicyNT);
+        const uint32_t lo = w[0], hi = w[1];
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
 template <class T>
 __device__ __forceinline__ void buf_st_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, T v)
 {

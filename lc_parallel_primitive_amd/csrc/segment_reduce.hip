@@ -12,22 +12,25 @@
 //  * A workgroup (4 waves) owns 256 consecutive segments, 64 per wave; lanes
 //    0..63 of a wave load the bounds of its segments with one coalesced load
 //    (or compute them, for fixed-size segments).
-//  * Wave-per-segment for segments up to kSegLong elements: the wave walks its
-//    64 segments 8 at a time; the 8 bounds are read out of the lanes into
-//    scalar registers and lane l accumulates elements l, l + 64, ... of each,
-//    two 64-element chunks per segment in flight (16 independent loads per
-//    lane); a 64-lane butterfly per segment leaves its result in the lane of
-//    that segment, and the wave stores its 64 results together.
-//  * Workgroup-per-segment for longer ones: their indices are compacted into
-//    LDS and the whole workgroup streams each one (4 loads in flight per
-//    thread) after its waves are done.  Fixed-size segments longer than
-//    kSegLong take a workgroup-per-segment launch directly.
-//  * Flat path: a wave whose 64 segments tile one contiguous range (CSR
-//    offsets with end[s] == begin[s + 1], or fixed-size segments), none of
-//    them long, streams that range in 4 KiB chunks of coalesced 16-byte
-//    loads, transposes each chunk through LDS so that every lane holds
-//    consecutive elements, folds them in order and joins the lanes with a
-//    segmented scan (flat_segments below).
+//  * Contiguous flat path: a wave whose 64 segments are sorted and disjoint
+//    (begin[s + 1] >= end[s]: CSR offsets that tile a range, or ranges with
+//    gaps that hold fewer elements than the segments), none of them long,
+//    streams the range from its first begin to its last end in 4 KiB chunks
+//    of coalesced 16-byte loads, transposes each chunk through LDS so that
+//    every lane holds consecutive elements, folds them in order restarting
+//    at each segment begin, and completes the segment open at each lane's
+//    start with a segmented scan (flat_segments below).
+//  * Gather path, every other layout (unsorted, overlapping, wide gaps, an
+//    input pointer that is not 16-byte aligned): the wave's segments are
+//    concatenated into one virtual range and the same fold runs over it;
+//    each chunk is gathered with one load per element, 64 consecutive
+//    virtual elements per wave load, each element's segment found from a
+//    bitmap of the segment ends in the chunk.  A wave whose segments lie
+//    more than 4 GiB apart folds one segment at a time instead.
+//  * Segments longer than kSegLong: their indices are compacted into LDS and
+//    the whole workgroup streams each one (4 loads in flight per thread)
+//    after its waves are done.  Fixed-size segments longer than kSegLong
+//    take a workgroup-per-segment launch directly.
 //  * Sum/Min/Max write op(init, fold) (init defaults to the operator's
 //    identity; Min starts from max(), Max from lowest()); an empty segment
 //    (end <= begin, or segment_size 0) writes init.  Arg* keep
@@ -47,18 +50,19 @@ namespace {
 
 constexpr int kSegBlock = 256;
 constexpr int kSegWaves = kSegBlock / kWave;
-// Segments in flight per wave and segments per wave.  Measured at C5
-// (2^27 f32, 2^20 segments of mean length 128, us): 4 / 8 / 16 in flight:
-// 128 / 118 / 142; 16 / 32 / 64 per wave: 121 / 119 / 117.  A persistent
-// grid of waves striding over groups of 8 measured 141-190 us, and 16-byte
-// vector loads with index masking 127 us (fewer waves fit).  The per-segment
-// wave reductions use DPP and readlane instead of __shfl_xor (ds_bpermute
-// through LDS): 119-122 -> 113 us.  The flat path takes C5 to 97 us (a copy
-// of it that only sums each wave's range, with no segment logic, runs in
-// 87.5 us): per-element branches 105 us, branch-free fold 99 us, segment of
-// each lane's first element by a 7-step binary search in LDS 99 us against
-// a slot histogram and a DPP scan 97 us.
-constexpr int kSegGroup = 8;
+// Measured at C5 (2^27 f32, 2^20 segments of mean length 128, us): a wave
+// walking its segments 8 at a time (one 64-lane load per segment and step)
+// 113-124; the contiguous flat path 94 (a copy of it that only sums each
+// wave's range, with no segment logic, runs in 87.5): per-element branches
+// 105, branch-free fold 99, segment of each lane's first element by a
+// binary search in LDS 99 against a slot histogram and a DPP scan 97.  Arg*
+// on the flat path: per-element branches 166-173, branch-free fold with the
+// arg positions packed in registers 111.  The same segments in a random
+// order (gather path): walking 124 (Sum) / 155 (Min) / 312 (ArgMin); gather
+// with each lane walking the segment ends in LDS 135 / 142 / 165, with a
+// scalar walk over the chunk's ends 131 / 135 / 173, with the end bitmap
+// and mbcnt 124 / 124 / 145 (gathering the tiling layout: 104; with no
+// segment lookup at all 96).
 constexpr int kSegPerWave = 64;
 constexpr uint32_t kSegLong = 8192;
 constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
@@ -208,28 +212,41 @@ __device__ __forceinline__ void wg_reduce_segment(const T *__restrict__ in, T *_
     __syncthreads();
 }
 
-// ---- flat path: a wave whose 64 segments tile one contiguous range
-// [B, E) streams that range in chunks with coalesced 16-byte loads instead
-// of walking its segments 8 at a time (24 dependent load round trips per
-// wave for mean length 128).  Each chunk goes through LDS so that lane l
-// then holds kFlatEpl consecutive elements; the lane folds them in order,
-// writing every segment that starts and ends inside it.  The open segment
-// at each lane's start comes from a segmented scan across the lanes (plus
-// the open segment carried from the previous chunk): with it a lane writes
-// the first segment that ends inside it.  The last segment of the range is
-// written after the last chunk, empty segments at the start.  Per segment the
-// fold order is the element order: first the lanes before, then the lane's
-// own elements.
+// ---- flat path: a wave whose 64 segments are sorted and do not overlap
+// (begin[s + 1] >= end[s]: CSR offsets that tile one range, or ranges with
+// gaps between them that hold fewer elements than the segments do) streams
+// the range [B, E) from its first begin to its last end in chunks with
+// coalesced 16-byte loads instead of walking its segments 8 at a time (24
+// dependent load round trips per wave for mean length 128).  Each chunk goes
+// through LDS so that lane l then holds EPL consecutive elements p0 .. p0 +
+// EPL - 1.  The lane folds them in order, restarting at every segment begin
+// inside it, and the fold at a segment's last element is that segment's
+// result when the segment began inside the lane.  The one segment that began
+// before p0 and ends inside the lane (the open segment) is completed with
+// the fold of the lanes before it, from a segmented scan restarted at the
+// segment begins (plus the fold carried over from the previous chunk).
+// Elements outside every segment (before B, in gaps, past E) are folded too
+// but never reach a result: every result is read from a fold that restarted
+// at its own segment's begin.  Empty segments are written at the start.  Per
+// segment the fold order is the element order.
 template <class T>
 constexpr int flat_epl()
 {
     return 64 / (int)sizeof(T);  // 4 KiB of elements per wave per chunk
 }
+// Largest range end the flat path takes: element indices of the last chunk
+// stay below 2^32.
+constexpr uint32_t kFlatMaxEnd = 0xFFFFFFFFu - 2u * kWave * 16u;
 template <class T>
 struct FlatSmem {
-    uint32_t bnd[kSegWaves][kSegPerWave + 1];
+    uint32_t bnd[kSegWaves][kSegPerWave + 1];   // begins (~0 past the wave's segments)
+    uint32_t ends[kSegWaves][kSegPerWave + 1];  // begin + length (~0 past them)
     uint32_t slots[kSegWaves][kWave];
     T stage[kSegWaves][kWave * (flat_epl<T>() + 1)];  // +1: conflict-free column reads
+    // gather: bitmap of the segment ends inside a chunk, one bit per virtual
+    // element, and the element-index offset of each non-empty segment
+    uint32_t gbits[kSegWaves][kWave * flat_epl<T>() / 32];
+    uint32_t gdelta[kSegWaves][kSegPerWave];
 };
 
 // Segmented inclusive scan of (flag, acc) pairs across the lanes (DPP steps
@@ -251,11 +268,38 @@ __device__ __forceinline__ void flat_seg_scan(bool &f, typename Acc::A &v)
     step(dpp_move<kDppRowBcast31, 0xC>((int)f, 0), Acc::template dpp_mv<kDppRowBcast31, 0xC>(v, id));
 }
 
-template <class T, int OP>
+// Whether the wave's segments take the flat path: sorted, not overlapping,
+// none long, gaps holding at most as many elements as the segments plus one
+// chunk, and a range end below kFlatMaxEnd.  Wave-uniform.
+template <class T>
+__device__ __forceinline__ bool flat_eligible(uint32_t nvalid, uint32_t b, uint32_t len)
+{
+    constexpr uint32_t CH = kWave * flat_epl<T>();
+    const uint32_t lane = lane_id();
+    const uint32_t b_next = (uint32_t)__shfl_down((int)b, 1);
+    const bool breaks = lane < nvalid && (len > kSegLong || (lane + 1 < nvalid && b + len > b_next));
+    if (nvalid == 0 || ballot(breaks) != 0) return false;
+    const uint32_t B = (uint32_t)__builtin_amdgcn_readfirstlane((int)b);
+    const uint32_t E = (uint32_t)__builtin_amdgcn_readlane((int)(b + len), (int)nvalid - 1);
+    const uint32_t total = wave_allreduce(lane < nvalid ? len : 0u, SumOp());  // <= 64 * kSegLong
+    return E <= kFlatMaxEnd && (uint64_t)(E - B) <= 2ull * total + CH;
+}
+
+// GATHER: the wave's segments in any layout, concatenated into one virtual
+// range (b, len: virtual begin and length; delta: element index minus
+// g_lo minus virtual index, where [g_lo, g_lo + g_bytes / sizeof(T)) holds
+// every element the wave reads).  Chunks are gathered with one load per
+// element, 64 consecutive virtual elements per wave load (one or two runs of
+// addresses); the fold runs on virtual indices, so Arg* positions relative
+// to a segment's begin are the same.  write_empty: whether a zero-length lane is an empty
+// segment to write (long segments, left to the workgroup path, are not).
+template <class T, int OP, bool GATHER>
 __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__restrict__ out,
                                               uint32_t *__restrict__ index_out, T init, uint64_t wseg0,
-                                              uint32_t nvalid, uint32_t b, uint32_t len, uint32_t *bnd,
-                                              uint32_t *slots, T *stage)
+                                              uint32_t nvalid, uint32_t b, uint32_t len, bool write_empty,
+                                              uint32_t delta, uint32_t g_lo, uint32_t g_bytes, uint32_t *bnd,
+                                              uint32_t *ends, uint32_t *slots, T *stage, uint32_t *gbits,
+                                              uint32_t *gdelta)
 {
     using Acc = SegAcc<T, OP>;
     using A = typename Acc::A;
@@ -263,39 +307,90 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
     constexpr int VEC = 16 / (int)sizeof(T);
     constexpr int LOADS = EPL / VEC;
     constexpr uint32_t CH = kWave * EPL;
+    // Arg*: the position (0 .. EPL - 1) of each prefix's arg element, 4 bits each
+    using PosBits = std::conditional_t<(EPL > 8), uint64_t, uint32_t>;
     const uint32_t lane = lane_id();
     const bool valid = lane < nvalid;
+    const uint32_t e = b + len;
     const uint32_t B = (uint32_t)__builtin_amdgcn_readfirstlane((int)b);
-    const uint32_t E = (uint32_t)__builtin_amdgcn_readlane((int)(b + len), (int)nvalid - 1);
-    bnd[lane] = valid ? b : E;
-    if (lane == 0) bnd[kSegPerWave] = E;
+    const uint32_t E = (uint32_t)__builtin_amdgcn_readlane((int)e, (int)nvalid - 1);
+    bnd[lane] = valid ? b : ~0u;
+    ends[lane] = valid ? e : ~0u;
+    if (lane == 0) {
+        bnd[kSegPerWave] = ~0u;
+        ends[kSegPerWave] = ~0u;
+    }
     __builtin_amdgcn_wave_barrier();
-    if (valid && len == 0) seg_store<T, OP>(Acc::identity(), b, init, out, index_out, wseg0 + lane);
+    if (valid && len == 0 && write_empty) seg_store<T, OP>(Acc::identity(), b, init, out, index_out, wseg0 + lane);
     const uint32_t A0 = B & ~(uint32_t)(VEC - 1);
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(in + A0, (E - A0) * (uint32_t)sizeof(T));  // reads past E give 0
+    // reads past E (contiguous) or outside [g_lo, ...) (gather) give 0
+    const __amdgpu_buffer_rsrc_t r =
+        GATHER ? make_rsrc(in + g_lo, g_bytes) : make_rsrc(in + A0, (E - A0) * (uint32_t)sizeof(T));
     const uint32_t nch = (E - A0 + CH - 1) / CH;
     auto emit = [&](uint32_t sid, A acc) { seg_store<T, OP>(acc, bnd[sid], init, out, index_out, wseg0 + sid); };
     A carry = Acc::identity();
-    // coalesced loads of chunk c: lane l, load k -> elements k*64*VEC + l*VEC .. + VEC - 1
-    u32x4 v[LOADS];
+    // contiguous: coalesced loads of chunk c, lane l, load k -> elements
+    // k*64*VEC + l*VEC .. + VEC - 1.  Gather: load j -> virtual element
+    // W + l (W = c*CH + j*64), read at W + l + the offset of the non-empty
+    // segment holding it.  That segment's rank among the non-empty ones is
+    // the count of non-empty segments whose last element lies before W + l:
+    // those before the chunk, plus bits of a bitmap of the chunk's last
+    // elements (the windows before this one, and this window's bits below
+    // the lane: mbcnt).  Loads past E read some element of [g_lo, ...) or 0:
+    // they only reach folds that never become results.
+    u32x4 v[GATHER ? 1 : LOADS];
+    T g[GATHER ? EPL : 1];
+    const bool nonempty = valid && len > 0;
+    const uint32_t gend = nonempty ? e : 0u;  // non-empty ends are distinct and >= 1
+    if constexpr (GATHER) {
+        const uint64_t ne = ballot(nonempty);
+        if (nonempty) gdelta[__builtin_popcountll(ne & ((1ull << lane) - 1))] = delta;
+    }
     auto load_chunk = [&](uint32_t c) {
+        if constexpr (GATHER) {
+            const uint32_t cb = c * CH;
+            if (lane < CH / 32) gbits[lane] = 0;
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t t = gend - 1u - cb;  // last element, chunk-relative
+            if (nonempty && t < CH) atomicOr(&gbits[t / 32], 1u << (t % 32));
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t word = lane < CH / 32 ? gbits[lane] : 0u;
+            uint32_t rank = (uint32_t)__builtin_popcountll(ballot(nonempty && gend <= cb));
 #pragma unroll
-        for (int k = 0; k < LOADS; ++k)
-            v[k] = buf_ld16_nt(r, (c * CH + (uint32_t)k * kWave * VEC + lane * VEC) * (uint32_t)sizeof(T), 0);
+            for (int j = 0; j < EPL; ++j) {
+                const uint32_t wlo = (uint32_t)__builtin_amdgcn_readlane((int)word, 2 * j);
+                const uint32_t whi = (uint32_t)__builtin_amdgcn_readlane((int)word, 2 * j + 1);
+                const uint32_t rk = __builtin_amdgcn_mbcnt_hi(whi, __builtin_amdgcn_mbcnt_lo(wlo, rank));
+                rank += (uint32_t)__builtin_popcount(wlo) + (uint32_t)__builtin_popcount(whi);
+                const uint32_t dl = gdelta[rk < kSegPerWave ? rk : kSegPerWave - 1];
+                g[j] = buf_ld_elem_nt<T>(r, (cb + (uint32_t)j * kWave + lane + dl) * (uint32_t)sizeof(T));
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < LOADS; ++k)
+                v[k] = buf_ld16_nt(r, (c * CH + (uint32_t)k * kWave * VEC + lane * VEC) * (uint32_t)sizeof(T), 0);
+        }
     };
     if (nch) load_chunk(0);
 #pragma unroll 1
     for (uint32_t c = 0; c < nch; ++c) {
         const uint32_t base = A0 + c * CH;  // element index of the chunk's first element
-        // chunk element q = k*64*VEC + lane*VEC + j belongs to lane q / EPL, position q % EPL
+        // chunk element q belongs to lane q / EPL, position q % EPL
+        if constexpr (GATHER) {
+            // q = j*64 + lane: row j*64/EPL + lane/EPL, column lane % EPL
+            T *srow = stage + (lane / EPL) * (EPL + 1) + lane % EPL;
 #pragma unroll
-        for (int k = 0; k < LOADS; ++k) {
-            T e[VEC];
-            unpack16<T>(v[k], e);
+            for (int j = 0; j < EPL; ++j) srow[j * (kWave / EPL) * (EPL + 1)] = g[j];
+        } else {
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                const uint32_t q = (uint32_t)k * kWave * VEC + lane * VEC + (uint32_t)j;
-                stage[(q / EPL) * (EPL + 1) + q % EPL] = e[j];
+            for (int k = 0; k < LOADS; ++k) {
+                T ev[VEC];
+                unpack16<T>(v[k], ev);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    const uint32_t q = (uint32_t)k * kWave * VEC + lane * VEC + (uint32_t)j;
+                    stage[(q / EPL) * (EPL + 1) + q % EPL] = ev[j];
+                }
             }
         }
         if (c + 1 < nch) load_chunk(c + 1);  // in flight while this chunk is folded
@@ -305,113 +400,131 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
         for (int j = 0; j < EPL; ++j) x[j] = stage[lane * (EPL + 1) + j];
         __builtin_amdgcn_wave_barrier();
 
-        // the segment holding element p0 - 1 is the last boundary below p0.
-        // Boundaries are counted per lane: boundary i (lane i's) is below
-        // the first element of every lane after slot (b_i - base) / EPL, so
-        // the count is a prefix sum of a 64-entry histogram of slots (those
-        // below the chunk counted by one ballot).
+        // i0 = the segments that end at or before p0 (ends are sorted), from a
+        // 64-entry histogram of the lanes whose first element follows each
+        // end, those below the chunk counted by one ballot
         const uint32_t p0 = base + lane * EPL;
-        const uint32_t bi = valid ? b : E;
-        const uint32_t below = (uint32_t)__builtin_popcountll(ballot(bi < base));
+        const uint32_t lim = p0 >= E ? E : (E - p0 < (uint32_t)EPL ? E : p0 + EPL);
+        const uint32_t below = (uint32_t)__builtin_popcountll(ballot(valid && e < base));
         slots[lane] = 0;
         __builtin_amdgcn_wave_barrier();
-        if (bi >= base && bi - base < CH - EPL) atomicAdd(&slots[(bi - base) / EPL + 1], 1u);
+        const uint32_t d = e - base;
+        if (valid && e >= base && d <= (uint32_t)(kWave - 1) * EPL) atomicAdd(&slots[(d + EPL - 1) / EPL], 1u);
         __builtin_amdgcn_wave_barrier();
-        const uint32_t cnt = below + wave_inclusive_scan(slots[lane], SumOp());
-        uint32_t sid = cnt > 0 ? (cnt - 1 < kSegPerWave ? cnt - 1 : kSegPerWave - 1) : 0u;
-        A acc = Acc::identity(), first_acc = Acc::identity();
-        uint32_t first_sid = 0;
-        bool seen = false;
-        if constexpr (!Acc::kArg) {
-            // branch-free: bit t of hmask = a segment starts at p0 + t; fold
-            // with restarts, values back into this lane's LDS row
-            const uint32_t lim = p0 + EPL < E ? p0 + EPL : E;
-            uint32_t hmask = 0;
-            {
-                uint32_t i = sid + 1, q = bnd[i];
-                while (q < lim) {
-                    hmask |= 1u << (q - p0);
-                    q = bnd[++i];
-                }
-            }
-            const uint32_t vlo = B > p0 ? B - p0 : 0u;
-            const uint32_t vhi = lim > p0 ? lim - p0 : 0u;
-            A v = Acc::identity();
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) {
-                const A xj = (uint32_t)j >= vlo && (uint32_t)j < vhi ? A(x[j]) : Acc::identity();
-                v = ((hmask >> j) & 1u) ? xj : Acc::combine(v, xj);
-                x[j] = v;
-            }
-            acc = v;
-            seen = hmask != 0;
-            if (__builtin_amdgcn_ballot_w64(seen)) {
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) stage[lane * (EPL + 1) + j] = x[j];
-                __builtin_amdgcn_wave_barrier();
-                if (seen) {
-                    // walk the boundaries again: the segment before each one
-                    // ends at t - 1; the first of them may have started in
-                    // earlier lanes (written after the scan below)
-                    uint32_t prev = sid, i = sid + 1, q = bnd[i];
-                    bool first = true;
-                    while (q < lim) {
-                        uint32_t q2 = bnd[i + 1];
-                        while (q2 == q) q2 = bnd[++i + 1];  // empty segments starting at q
-                        const uint32_t t = q - p0;
-                        const A val = t ? A(stage[lane * (EPL + 1) + t - 1]) : Acc::identity();
-                        if (first) {
-                            first_sid = prev;
-                            first_acc = val;
-                            first = false;
-                        } else {
-                            emit(prev, val);
-                        }
-                        prev = i++;
-                        q = q2;
-                    }
-                }
-                __builtin_amdgcn_wave_barrier();
-            }
-        } else {
-            uint32_t nb = bnd[sid + 1];
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) {
-                const uint32_t p = p0 + (uint32_t)j;
-                if (p >= B && p < E) {
-                    if (p == nb) {  // segment sid ended at p - 1
-                        if (!seen) {
-                            first_sid = sid;
-                            first_acc = acc;
-                            seen = true;
-                        } else {
-                            emit(sid, acc);
-                        }
-                        do {  // skip the empty segments that start and end at p
-                            ++sid;
-                            nb = bnd[sid + 1];
-                        } while (nb == p);
-                        acc = Acc::identity();
-                    }
-                    acc = Acc::fold(acc, x[j], p);
-                }
+        const uint32_t i0 = below + wave_inclusive_scan(slots[lane], SumOp());
+        // bit t of hmask: a segment begins at p0 + t (only segment i0 can
+        // have begun before p0; every later one begins after its end > p0)
+        uint32_t hmask = 0;
+        {
+            uint32_t i = i0, q = bnd[i];
+            if (q < p0) q = bnd[++i];
+            while (q < lim) {
+                hmask |= 1u << (q - p0);
+                q = bnd[++i];
             }
         }
+        // in-order fold with restarts; the lane's own prefix folds stay
+        // readable at every position (Sum/Min/Max: in LDS; Arg*: the element
+        // positions in pos, the values still in LDS)
+        A lane_acc;
+        PosBits pos = 0;
+        if constexpr (!Acc::kArg) {
+            T run = x[0];
+#pragma unroll
+            for (int j = 1; j < EPL; ++j) {
+                run = ((hmask >> j) & 1u) ? x[j] : Acc::combine(run, x[j]);
+                x[j] = run;
+            }
+            lane_acc = run;
+        } else {
+            T av = x[0];
+            uint32_t ap = 0;
+#pragma unroll
+            for (int j = 1; j < EPL; ++j) {
+                // in-order fold: the later element wins ties only for ArgMax
+                const bool better = OP == kSegArgMax ? x[j] >= av : x[j] < av;
+                const bool take = ((hmask >> j) & 1u) || better;
+                av = take ? x[j] : av;
+                ap = take ? (uint32_t)j : ap;
+                pos |= (PosBits)ap << (4 * j);
+            }
+            lane_acc = A{av, p0 + ap};
+        }
+        auto prefix_at = [&](uint32_t t) -> A {
+            if constexpr (!Acc::kArg) {
+                return stage[lane * (EPL + 1) + t];
+            } else {
+                const uint32_t pt = (uint32_t)(pos >> (4 * t)) & 15u;
+                return A{stage[lane * (EPL + 1) + pt], p0 + pt};
+            }
+        };
+        // segments ending inside the lane (last element in [p0, lim))
+        const uint32_t e0 = ends[i0];
+        const bool has_end = e0 <= lim;
+        if constexpr (!Acc::kArg) {
+            if (ballot(has_end)) {
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) stage[lane * (EPL + 1) + j] = x[j];
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        bool has_first = false;
+        uint32_t first_sid = 0;
+        A first_acc = Acc::identity();
+        if (has_end) {
+            uint32_t i = i0, ee = e0;
+            do {
+                const uint32_t bi = bnd[i];
+                if (ee > bi) {  // empty segments were written at the start
+                    const A val = prefix_at(ee - 1 - p0);
+                    if (bi < p0) {
+                        has_first = true;
+                        first_sid = i;
+                        first_acc = val;
+                    } else {
+                        emit(i, val);
+                    }
+                }
+                ee = ends[++i];
+            } while (ee <= lim);
+        }
+        __builtin_amdgcn_wave_barrier();  // LDS reads done before the next chunk's stage writes
         // open segment at each lane's start: carry, then the lanes before
-        bool f = seen;
-        A inc = acc;
+        bool f = hmask != 0;
+        A inc = lane_acc;
         flat_seg_scan<Acc>(f, inc);
         const int fprev = wave_shr1((int)f, 0);
         const A iprev = Acc::template dpp_mv<kDppWaveShr1, 0xF>(inc, Acc::identity());
         const A open = lane == 0 ? carry : (fprev ? iprev : Acc::combine(carry, iprev));
-        if (seen) emit(first_sid, Acc::combine(open, first_acc));
+        if (has_first) emit(first_sid, Acc::combine(open, first_acc));
         const bool f63 = __builtin_amdgcn_readlane((int)f, kWave - 1) != 0;
         const A i63 = Acc::readlane_acc(inc, kWave - 1);
         carry = f63 ? i63 : Acc::combine(carry, i63);
     }
-    // the range's last non-empty segment ends at E
-    const uint64_t ne = ballot(valid && len > 0);
-    if (ne && lane == 0) emit(63u - (uint32_t)__builtin_clzll(ne), carry);
+}
+
+// A wave whose segments lie more than 4 GiB apart: one segment at a time,
+// lane l folding elements l, l + 64, ... (long segments are left to the
+// workgroup path).
+template <class T, int OP>
+__device__ __forceinline__ void wave_segments(const T *__restrict__ in, T *__restrict__ out,
+                                              uint32_t *__restrict__ index_out, T init, uint64_t wseg0,
+                                              uint32_t nvalid, uint32_t b, uint32_t len)
+{
+    using Acc = SegAcc<T, OP>;
+    using A = typename Acc::A;
+    const uint32_t lane = lane_id();
+#pragma unroll 1
+    for (uint32_t s = 0; s < nvalid; ++s) {
+        const uint32_t bs = (uint32_t)__builtin_amdgcn_readlane((int)b, (int)s);
+        const uint32_t ls = (uint32_t)__builtin_amdgcn_readlane((int)len, (int)s);
+        if (ls > kSegLong) continue;
+        A acc = Acc::identity();
+#pragma unroll 1
+        for (uint32_t i = lane; i < ls; i += kWave) acc = Acc::fold(acc, in[(uint64_t)bs + i], bs + i);
+        const A res = Acc::wave_reduce(acc);
+        if (lane == 0) seg_store<T, OP>(res, bs, init, out, index_out, wseg0 + s);
+    }
 }
 
 template <class T, int OP, bool FIXED>
@@ -437,57 +550,28 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__re
     const bool is_long = len > kSegLong;
     if (is_long) s_long[atomicAdd(&s_nlong, 1u)] = (uint32_t)(wave * kSegPerWave + lane);
 
-    // flat path when the wave's segments tile one range and none is long
+    // contiguous flat path when the wave's segments are sorted, disjoint and
+    // none is long; else the gather form over the concatenated segments
     const uint32_t nvalid = wseg0 < S ? (uint32_t)(S - wseg0 < kSegPerWave ? S - wseg0 : kSegPerWave) : 0u;
-    const uint32_t b_next = (uint32_t)__shfl_down((int)b, 1);
-    const bool breaks = lane < nvalid && (len > kSegLong || (lane + 1 < nvalid && b + len != b_next));
-    if (vec_ok && nvalid > 0 && ballot(breaks) == 0) {
-        flat_segments<T, OP>(in, out, index_out, init, wseg0, nvalid, b, len, s_flat.bnd[wave], s_flat.slots[wave],
-                             s_flat.stage[wave]);
-    } else {
-    A mine = Acc::identity();
-#pragma unroll 1
-    for (int j0 = 0; j0 < kSegPerWave; j0 += kSegGroup) {
-        uint32_t bj[kSegGroup], lj[kSegGroup];
-        uint32_t maxlen = 0;
-#pragma unroll
-        for (int u = 0; u < kSegGroup; ++u) {
-            bj[u] = __builtin_amdgcn_readlane(b, j0 + u);
-            const uint32_t l = __builtin_amdgcn_readlane(len, j0 + u);
-            lj[u] = l > kSegLong ? 0u : l;  // long segments: workgroup path below
-            maxlen = lj[u] > maxlen ? lj[u] : maxlen;
+    if (vec_ok && flat_eligible<T>(nvalid, b, len)) {
+        flat_segments<T, OP, false>(in, out, index_out, init, wseg0, nvalid, b, len, true, 0u, 0u, 0u,
+                                    s_flat.bnd[wave], s_flat.ends[wave], s_flat.slots[wave], s_flat.stage[wave],
+                                    s_flat.gbits[wave], s_flat.gdelta[wave]);
+    } else if (nvalid > 0) {
+        const uint32_t vlen = is_long ? 0u : len;
+        // elements the gather reads: [lo, hi), at most 4 GiB for one buffer resource
+        uint32_t lo = wave_allreduce(vlen ? b : ~0u, MinOp());
+        const uint32_t hi = wave_allreduce(vlen ? b + vlen : 0u, MaxOp());
+        if (hi <= lo) lo = 0;  // nothing to read
+        const uint64_t bytes = hi > lo ? (uint64_t)(hi - lo) * sizeof(T) : 0;
+        if (bytes <= 0xFFFFFFFFull) {
+            const uint32_t vb = wave_inclusive_scan(vlen, SumOp()) - vlen;  // <= 64 * kSegLong
+            flat_segments<T, OP, true>(in, out, index_out, init, wseg0, nvalid, vb, vlen, !is_long, b - lo - vb, lo,
+                                       (uint32_t)bytes, s_flat.bnd[wave], s_flat.ends[wave], s_flat.slots[wave],
+                                       s_flat.stage[wave], s_flat.gbits[wave], s_flat.gdelta[wave]);
+        } else {
+            wave_segments<T, OP>(in, out, index_out, init, wseg0, nvalid, b, len);
         }
-        if (maxlen == 0) continue;
-        A acc[kSegGroup];
-#pragma unroll
-        for (int u = 0; u < kSegGroup; ++u) acc[u] = Acc::identity();
-#pragma unroll 1
-            for (uint32_t c = lane; c < maxlen; c += 2 * kWave) {
-                T x0[kSegGroup], x1[kSegGroup];
-#pragma unroll
-                for (int u = 0; u < kSegGroup; ++u) {
-                    x0[u] = c < lj[u] ? in[(uint64_t)bj[u] + c] : T(0);
-                    x1[u] = c + kWave < lj[u] ? in[(uint64_t)bj[u] + c + kWave] : T(0);
-                }
-#pragma unroll
-                for (int u = 0; u < kSegGroup; ++u) {
-                    if constexpr (OP == kSegSum) {
-                        acc[u] = Acc::fold(Acc::fold(acc[u], x0[u], 0), x1[u], 0);  // out-of-range loads are 0
-                    } else {
-                        if (c < lj[u]) acc[u] = Acc::fold(acc[u], x0[u], bj[u] + c);
-                        if (c + kWave < lj[u]) acc[u] = Acc::fold(acc[u], x1[u], bj[u] + c + kWave);
-                    }
-                }
-            }
-#pragma unroll
-        for (int u = 0; u < kSegGroup; ++u) {
-            if (lj[u] == 0) continue;
-            const A r = Acc::wave_reduce(acc[u]);
-            if (lane == (uint32_t)(j0 + u)) mine = r;
-        }
-    }
-    if (lane < (uint32_t)kSegPerWave && wseg0 + lane < S && !is_long)
-        seg_store<T, OP>(mine, b, init, out, index_out, wseg0 + lane);
     }
 
     // ---- long segments: the whole workgroup streams each one

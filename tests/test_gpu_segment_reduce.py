@@ -294,3 +294,118 @@ def test_contiguous_then_scattered_waves(gpu):
     b, e = np.concatenate([b1, b2]), np.concatenate([e1, e2])
     a = g.random_array(np.int32, n, seed=5)
     assert (run(g.to_dev(a), b, e, np.int32) == o.segment_reduce(o.OP_SUM, a, b, e)).all()
+
+
+# ------------------------------------------------------------------ layouts that do not tile one range
+def gapped_layout(lengths, gaps):
+    """Sorted, disjoint CSR ranges: segment i is followed by gaps[i] elements
+    that belong to no segment."""
+    L = np.asarray(lengths, dtype=np.int64)
+    G = np.asarray(gaps, dtype=np.int64)
+    b = np.concatenate([[0], np.cumsum(L + G)[:-1]])
+    return b.astype(np.uint32), (b + L).astype(np.uint32)
+
+
+def _nontiling_layouts():
+    rng = np.random.default_rng(123)
+    geo = rng.geometric(1 / 100, 1500) - 1  # mean ~99, ~1 % empty
+    short = rng.integers(0, 4, 3000)  # several ends per 64-element window
+    tb, te = contiguous_layout(geo)
+    perm = rng.permutation(geo.size)
+    sb, se = contiguous_layout(short)
+    sperm = rng.permutation(short.size)
+    lay = {
+        # sorted with gaps: the contiguous path reads the gaps and drops them
+        "gaps_one": gapped_layout(geo, np.ones(geo.size, np.int64)),
+        "gaps_mixed": gapped_layout(geo, rng.integers(0, 40, geo.size) * (rng.random(geo.size) < 0.3)),
+        # gaps holding more elements than the segments: gather
+        "gaps_too_wide": gapped_layout(rng.integers(0, 10, 900), np.full(900, 200)),
+        # not sorted: gather
+        "permuted": (tb[perm], te[perm]),
+        "short_permuted": (sb[sperm], se[sperm]),
+        "descending": (tb[::-1].copy(), te[::-1].copy()),
+    }
+    # sorted and overlapping (sliding windows of 1..300 elements, stride 50)
+    ob = (np.arange(2000, dtype=np.int64) * 50).astype(np.uint32)
+    lay["sliding_windows"] = (ob, (ob + rng.integers(1, 300, ob.size)).astype(np.uint32))
+    # sorted and disjoint, with inverted ranges (end < begin: empty) between them
+    ib, ie = gapped_layout(geo, rng.integers(0, 3, geo.size))
+    ie = ie.copy()
+    ie[::10] = ib[::10] - np.minimum(ib[::10], 5)
+    lay["gaps_inverted_empty"] = (ib, ie)
+    return lay
+
+
+NONTILING = _nontiling_layouts()
+
+
+@pytest.mark.parametrize("layout", sorted(NONTILING))
+@pytest.mark.parametrize("dtype", [np.int32, np.float32, np.int64, np.float64])
+@pytest.mark.parametrize("pad", [0, 1])
+def test_nontiling_layouts_all_ops(gpu, layout, dtype, pad):
+    import gpu_util as g
+
+    b, e = NONTILING[layout]
+    n = int(max(e.max(), b.max())) + 7
+    rng = np.random.default_rng(n + pad)
+    a = rng.integers(-40, 40, n).astype(dtype)  # ties; float sums of small integers are exact in any order
+    d = g.to_dev(a, pad=pad)  # pad = 1: 16-byte loads are off, every wave gathers
+    S = b.size
+    log(f"segment nontiling {layout} {np.dtype(dtype).name} pad={pad}")
+    for method, op in (("Sum", o.OP_SUM), ("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        assert same(seg_call(method, d, S, (b, e), dtype), o.segment_reduce(op, a, b, e)), method
+    for method, is_max in (("ArgMin", False), ("ArgMax", True)):
+        v, i = seg_call(method, d, S, (b, e), dtype, arg=True)
+        ev, ei = o.segment_reduce_arg(is_max, a, b, e)
+        assert same(v, ev) and (i == ei).all(), method
+
+
+def test_nontiling_full_size_permuted(gpu):
+    """C5's segments in a random order (every wave gathers) at full size:
+    Sum within the float64 bound, ArgMax exact."""
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n, S = 1 << 27, 1 << 20
+    log("segment f32 full 2^27 / 2^20 permuted")
+    d = datagen.normal_f32(n, seed=datagen.SEED_SEG_VALUES)
+    b, e = datagen.segments(n, S)
+    perm = np.random.default_rng(3).permutation(S)
+    b, e = b[perm].copy(), e[perm].copy()
+    got = run(d, b, e, np.float32)
+    h = g.to_host(d)
+    s, ab = o.segment_reduce_f64(h, b, e)
+    assert (np.abs(got.astype(np.float64) - s) <= RTOL_SEG * ab).all()
+    v, i = seg_call("ArgMax", d, S, (b, e), np.float32, arg=True)
+    ev, ei = o.segment_reduce_arg(True, h, b, e)
+    assert same(v, ev) and (i == ei).all()
+
+
+def test_segments_more_than_4gib_apart(gpu):
+    """A wave whose segments lie more than 4 GiB apart (int32 input of 2^30 +
+    2^20 elements, value = index) takes the one-segment-at-a-time path:
+    results from closed forms."""
+    import torch
+
+    import gpu_util as g
+
+    n = (1 << 30) + (1 << 20)
+    log("segment int32 2^30+2^20 segments > 4 GiB apart")
+    d = torch.arange(n, dtype=torch.int32, device="cuda")
+    S = 200
+    rng = np.random.default_rng(8)
+    L = rng.integers(0, 300, S)
+    L[5] = 0
+    L[17] = 9000  # long: workgroup path
+    b = np.where(np.arange(S) % 2 == 0, np.arange(S) * 400, n - 20_000 + np.arange(S) * 90).astype(np.int64)
+    e = np.minimum(b + L, n)
+    bu, eu = b.astype(np.uint32), e.astype(np.uint32)
+    sums = [(int((x + y - 1) * (y - x) // 2)) if y > x else 0 for x, y in zip(b, e)]
+    expect_sum = np.array([(v + 2**31) % 2**32 - 2**31 for v in sums], dtype=np.int64).astype(np.int32)
+    assert (seg_call("Sum", d, S, (bu, eu), np.int32) == expect_sum).all()
+    empty = e <= b
+    mn = seg_call("Min", d, S, (bu, eu), np.int32)
+    assert (mn[~empty] == b[~empty]).all() and (mn[empty] == np.iinfo(np.int32).max).all()
+    v, i = seg_call("ArgMax", d, S, (bu, eu), np.int32, arg=True)
+    assert (v[~empty] == e[~empty] - 1).all() and (i[~empty] == (e - b - 1)[~empty]).all()
+    assert (i[empty] == 1).all()
