@@ -71,3 +71,52 @@ def test_threads_distinct_temp_and_streams(gpu):
         cs = np.concatenate([[0], np.cumsum(j["x"], dtype=np.int64)])
         want = ((cs[j["end"]] - cs[j["begin"]]) & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
         assert (g.to_host(j["go"]) == want).all()
+
+
+def test_concurrent_large_sorts(gpu):
+    """Four streams each queue four 2^24-key sorts (1024 tiles each, far more
+    than one sort's 128-workgroup look-ahead) without waiting in between, so
+    the sorts overlap on the GPU: every call's status word must read OK and
+    its output must be the sorted permutation of its input."""
+    import ctypes
+
+    import torch
+
+    import gpu_util as g
+    import lc_parallel_primitive_amd as lcpp
+    from lc_parallel_primitive_amd import DeviceRadixSort
+
+    n, rounds = 1 << 24, 4
+    L = lcpp.lib()
+    tb = DeviceRadixSort.GetSortKeysTempStorageBytes("uint32", n)
+    jobs = []
+    for t in range(THREADS):
+        k = g.random_array(np.uint32, n, seed=400 + t)
+        jobs.append(dict(k=k, dk=g.to_dev(k), ko=[g.empty(n, np.uint32) for _ in range(rounds)],
+                         temp=[g.temp(tb) for _ in range(rounds)], stream=torch.cuda.Stream()))
+    torch.cuda.synchronize()
+    errors = []
+    barrier = threading.Barrier(THREADS)
+
+    def work(j):
+        try:
+            barrier.wait()
+            for r in range(rounds):
+                DeviceRadixSort().SortKeys(j["temp"][r], j["dk"], j["ko"][r], n, stream=j["stream"])
+        except Exception as e:  # reported on the main thread
+            errors.append(e)
+
+    log(f"concurrency: {THREADS} streams x {rounds} queued SortKeys of n={n}")
+    threads = [threading.Thread(target=work, args=(j,)) for j in jobs]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for t, j in enumerate(jobs):
+        for r in range(rounds):
+            st = L.lcpp_temp_status(ctypes.c_void_p(j["temp"][r].data_ptr()), j["temp"][r].numel(),
+                                    ctypes.c_void_p(j["stream"].cuda_stream))
+            assert st == 0, (t, r, st)
+            assert o.check_sorted_permutation_u32(j["k"], g.to_host(j["ko"][r])), (t, r)
