@@ -1,0 +1,175 @@
+"""The primitives under HIP graph capture (torch.cuda.graph on the current
+stream): each call is captured once and replayed several times, the input
+rewritten eagerly between replays, with unrelated eager work and a
+synchronization between them; every replay is checked against the oracle for
+the input it saw.  The library records only kernels (no memset nodes, no host
+synchronization) and each call's first kernel re-zeroes the status word and
+look-back state it owns, so replays need no host step."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import log
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+REPLAYS = 3
+
+
+def _replay_and_check(name, call, set_input, check):
+    """call(): the primitive on the current stream; set_input(r): eager rewrite
+    of the inputs for replay r (r = -1: the warm-up call); check(r): host
+    comparison after replay r."""
+    import torch
+
+    set_input(-1)
+    call()  # eager warm-up: the library's one-time launch facts are cached outside the capture
+    torch.cuda.synchronize()
+    check(-1)
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g):
+            call()
+    torch.cuda.synchronize()
+    for r in range(REPLAYS):
+        set_input(r)
+        noise = torch.randn(1 << 20, device="cuda")  # eager work between replays
+        noise.mul_(2).sum()
+        torch.cuda.synchronize()
+        log(f"graph {name} replay {r}")
+        g.replay()
+        torch.cuda.synchronize()
+        check(r)
+
+
+def test_graph_sort_keys_and_pairs(gpu):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceRadixSort
+
+    n = 1_000_003
+    dk, ko = g.empty(n, np.uint32), g.empty(n, np.uint32)
+    t = g.temp(DeviceRadixSort.GetSortKeysTempStorageBytes("uint32", n))
+    host = {}
+
+    def set_input(r):
+        host["k"] = g.random_array(np.uint32, n, seed=1000 + r)
+        dk.copy_(g.to_dev(host["k"]))
+
+    _replay_and_check("SortKeys u32", lambda: DeviceRadixSort().SortKeys(t, dk, ko, n), set_input,
+                      lambda r: np.testing.assert_array_equal(g.to_host(ko), np.sort(host["k"])))
+
+    # 8-byte keys whose upper 48 bits are zero: the device-side pass plan skips
+    # six passes, decided afresh in every replay
+    m = 300_007
+    k64, ko64 = g.empty(m, np.uint64), g.empty(m, np.uint64)
+    v, vo = g.empty(m, np.uint32), g.empty(m, np.uint32)
+    tp = g.temp(DeviceRadixSort.GetSortPairsTempStorageBytes("uint64", "uint32", m))
+
+    def set_pairs(r):
+        rng = np.random.default_rng(2000 + r)
+        host["k64"] = rng.integers(0, 1 << 16, m, dtype=np.uint64) << np.uint64(8 * (r % 2))
+        k64.copy_(g.to_dev(host["k64"]))
+        v.copy_(g.to_dev(np.arange(m, dtype=np.uint32)))
+
+    def check_pairs(r):
+        rk, rv = o.radix_sort(host["k64"], np.arange(m, dtype=np.uint32))
+        np.testing.assert_array_equal(g.to_host(ko64), rk)
+        np.testing.assert_array_equal(g.to_host(vo), rv)
+
+    _replay_and_check("SortPairs u64->u32", lambda: DeviceRadixSort().SortPairs(tp, k64, ko64, v, vo, m),
+                      set_pairs, check_pairs)
+
+
+def test_graph_scan_reduce_noalloc(gpu):
+    import gpu_util as g
+    import lc_parallel_primitive_amd as lcpp
+    from lc_parallel_primitive_amd import DeviceReduce, DeviceScan
+
+    n = 3_000_017
+    x, y, z = g.empty(n, np.int32), g.empty(n, np.int32), g.empty(n, np.int32)
+    s, idx, mn = g.empty(1, np.int32), g.empty(1, np.uint32), g.empty(1, np.int32)
+    ts = g.temp(DeviceScan.GetTempStorageBytes("int32", n))
+    tr = g.temp(DeviceReduce.GetTempStorageBytes("int32", n))
+    ta = g.temp(DeviceReduce.GetArgTempStorageBytes("int32", n))
+    L = lcpp.lib()
+    host = {}
+
+    def call():
+        DeviceScan().InclusiveSum(ts, x, y, n)
+        DeviceReduce().Sum(tr, x, s, n)
+        DeviceReduce().ArgMin(ta, x, mn, idx, n)
+        import torch
+
+        rc = L.lcpp_scan_exclusive_sum_noalloc(0, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(z.data_ptr()), n,
+                                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, rc
+
+    def set_input(r):
+        host["x"] = g.random_array(np.int32, n, seed=3000 + r)
+        x.copy_(g.to_dev(host["x"]))
+
+    def check(r):
+        a = host["x"]
+        c = np.cumsum(a, dtype=np.int32)
+        np.testing.assert_array_equal(g.to_host(y), c)
+        np.testing.assert_array_equal(g.to_host(z), np.concatenate([[0], c[:-1]]).astype(np.int32))
+        assert g.to_host(s)[0] == a.sum(dtype=np.int32)
+        assert g.to_host(mn)[0] == a.min() and g.to_host(idx)[0] == int(np.argmin(a))
+
+    _replay_and_check("scans and reduces", call, set_input, check)
+
+
+def test_graph_by_key_and_segments(gpu):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce, DeviceScan, DeviceSegmentReduce
+
+    n = 2_000_003
+    k, v = g.empty(n, np.int32), g.empty(n, np.int32)
+    sbk, uk, ag = g.empty(n, np.int32), g.empty(n, np.int32), g.empty(n, np.int32)
+    nr = g.empty(1, np.uint32)
+    tsk = g.temp(DeviceScan.GetScanByKeyTempStorageBytes("int32", "int32", n))
+    trk = g.temp(DeviceReduce.GetReduceByKeyTempStorageBytes("int32", "int32", n))
+    S = 20_000
+    b, e = g.empty(S, np.uint32), g.empty(S, np.uint32)
+    so, ao, ai = g.empty(S, np.int32), g.empty(S, np.int32), g.empty(S, np.uint32)
+    host = {}
+
+    def call():
+        DeviceScan().InclusiveSumByKey(tsk, k, v, sbk, n)
+        DeviceReduce().ReduceByKey(trk, k, v, uk, ag, nr, "sum", n)
+        DeviceSegmentReduce().Sum(None, v, so, S, b, e)
+        DeviceSegmentReduce().ArgMin(None, v, ao, ai, S, b, e)
+
+    def set_input(r):
+        rng = np.random.default_rng(4000 + r)
+        keys = np.cumsum(rng.random(n) < 1 / (5 + 40 * (r + 1))).astype(np.int32)  # runs, their length varies per replay
+        vals = rng.integers(-1000, 1000, n).astype(np.int32)
+        bb = np.sort(rng.integers(0, n, S)).astype(np.uint32)
+        ee = np.minimum(bb.astype(np.int64) + rng.integers(0, 400, S), n).astype(np.uint32)
+        if r % 2:
+            perm = rng.permutation(S)  # odd replays: segments in a random order (gather path)
+            bb, ee = bb[perm].copy(), ee[perm].copy()
+        host.update(k=keys, v=vals, b=bb, e=ee)
+        k.copy_(g.to_dev(keys))
+        v.copy_(g.to_dev(vals))
+        b.copy_(g.to_dev(bb))
+        e.copy_(g.to_dev(ee))
+
+    def check(r):
+        keys, vals, bb, ee = host["k"], host["v"], host["b"], host["e"]
+        np.testing.assert_array_equal(g.to_host(sbk), o.scan_by_key(keys, vals, True))
+        ruk, rag = o.reduce_by_key(keys, vals)
+        runs = int(g.to_host(nr)[0])
+        assert runs == ruk.size
+        np.testing.assert_array_equal(g.to_host(uk)[:runs], ruk)
+        np.testing.assert_array_equal(g.to_host(ag)[:runs], rag)
+        np.testing.assert_array_equal(g.to_host(so), o.segment_reduce(o.OP_SUM, vals, bb, ee))
+        ev, ei = o.segment_reduce_arg(False, vals, bb, ee)
+        np.testing.assert_array_equal(g.to_host(ao), ev)
+        np.testing.assert_array_equal(g.to_host(ai), ei)
+
+    _replay_and_check("by-key and segments", call, set_input, check)
