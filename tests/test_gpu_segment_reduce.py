@@ -409,3 +409,45 @@ def test_segments_more_than_4gib_apart(gpu):
     v, i = seg_call("ArgMax", d, S, (bu, eu), np.int32, arg=True)
     assert (v[~empty] == e[~empty] - 1).all() and (i[~empty] == (e - b - 1)[~empty]).all()
     assert (i[empty] == 1).all()
+
+
+def test_segments_at_the_top_of_the_32_bit_range(gpu):
+    """Segments ending at element 2^32 - 1 (an int32 input of 2^32 - 1
+    elements, 16 GiB): a tiling layout there is past the contiguous path's
+    range limit and gathers; element indices near 2^32 must not wrap.  Values
+    are 1 except a few marked elements, so sums are lengths plus marks and
+    ArgMax finds the marks."""
+    import torch
+
+    n = (1 << 32) - 1
+    log("segment int32 2^32-1 elements, segments at the top")
+    d = torch.ones(n, dtype=torch.int32, device="cuda")
+    rng = np.random.default_rng(12)
+    L = rng.integers(0, 200, 300)
+    L[7] = 0
+    e_last = n
+    e = e_last - np.concatenate([[0], np.cumsum(L[::-1])[:-1]])[::-1]
+    b = e - L
+    b, e = b.astype(np.int64), e.astype(np.int64)
+    marks = {int(b[i] + L[i] // 2): 1000 + i for i in range(0, 300, 5) if L[i] > 0}
+    marks[n - 1] = 7777  # the very last element
+    for pos, v in marks.items():
+        d[pos] = v
+    bu, eu = b.astype(np.uint32), e.astype(np.uint32)
+    S = b.size
+    want = L.astype(np.int64).copy()
+    for s_ in range(S):
+        for pos, v in marks.items():
+            if b[s_] <= pos < e[s_]:
+                want[s_] += v - 1
+    assert (seg_call("Sum", d, S, (bu, eu), np.int32) == want.astype(np.int32)).all()
+    v, i = seg_call("ArgMax", d, S, (bu, eu), np.int32, arg=True)
+    for s_ in range(S):
+        ms = [(val, pos) for pos, val in marks.items() if b[s_] <= pos < e[s_]]
+        if ms:
+            val, pos = max(ms)
+            assert v[s_] == val and i[s_] == pos - b[s_]
+        elif L[s_] > 0:
+            assert v[s_] == 1 and i[s_] == L[s_] - 1  # ties: the largest index
+    del d
+    torch.cuda.empty_cache()
