@@ -57,12 +57,13 @@ constexpr int kSegWaves = kSegBlock / kWave;
 // 105, branch-free fold 99, segment of each lane's first element by a
 // binary search in LDS 99 against a slot histogram and a DPP scan 97.  Arg*
 // on the flat path: per-element branches 166-173, branch-free fold with the
-// arg positions packed in registers 111.  The same segments in a random
+// arg positions packed in registers 111, combining in element order (one
+// empty check, no index tie break) 104.  The same segments in a random
 // order (gather path): walking 124 (Sum) / 155 (Min) / 312 (ArgMin); gather
 // with each lane walking the segment ends in LDS 135 / 142 / 165, with a
 // scalar walk over the chunk's ends 131 / 135 / 173, with the end bitmap
-// and mbcnt 124 / 124 / 145 (gathering the tiling layout: 104; with no
-// segment lookup at all 96).
+// and mbcnt 124 / 124 / 145, with the ordered combine 123 / 125 / 136
+// (gathering the tiling layout: 104; with no segment lookup at all 96).
 constexpr int kSegPerWave = 64;
 constexpr uint32_t kSegLong = 8192;
 constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
@@ -98,6 +99,18 @@ struct SegAcc {
             if (a.index == kNoIndex) return b;
             const bool take = OP == kSegArgMax ? (b.value > a.value || (b.value == a.value && b.index > a.index))
                                                : (b.value < a.value || (b.value == a.value && b.index < a.index));
+            return take ? b : a;
+        }
+    }
+    // a then b in element order (every index of b above every index of a),
+    // b not the identity: Arg* need neither b's empty check nor the index tie
+    // break (the earlier pair wins a tie for ArgMin, the later for ArgMax)
+    static __device__ __forceinline__ A combine_ordered(A a, A b)
+    {
+        if constexpr (!kArg) {
+            return combine(a, b);
+        } else {
+            const bool take = a.index == kNoIndex || (OP == kSegArgMax ? b.value >= a.value : b.value < a.value);
             return take ? b : a;
         }
     }
@@ -250,14 +263,16 @@ struct FlatSmem {
 };
 
 // Segmented inclusive scan of (flag, acc) pairs across the lanes (DPP steps
-// of wave_inclusive_scan): a flagged lane restarts the fold.
+// of wave_inclusive_scan): a flagged lane restarts the fold.  Every lane's
+// acc holds at least one element (lanes without a DPP source get the
+// identity, which the ordered combine passes over).
 template <class Acc>
 __device__ __forceinline__ void flat_seg_scan(bool &f, typename Acc::A &v)
 {
     using A = typename Acc::A;
     const A id = Acc::identity();
     auto step = [&](int fu, A vu) {
-        v = f ? v : Acc::combine(vu, v);
+        v = f ? v : Acc::combine_ordered(vu, v);
         f = f || fu != 0;
     };
     step(dpp_move<kDppRowShr + 1>((int)f, 0), Acc::template dpp_mv<kDppRowShr + 1, 0xF>(v, id));
@@ -307,8 +322,9 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
     constexpr int VEC = 16 / (int)sizeof(T);
     constexpr int LOADS = EPL / VEC;
     constexpr uint32_t CH = kWave * EPL;
-    // Arg*: the position (0 .. EPL - 1) of each prefix's arg element, 4 bits each
-    using PosBits = std::conditional_t<(EPL > 8), uint64_t, uint32_t>;
+    // Arg*: the position (0 .. EPL - 1) of each prefix's arg element, 4 bits
+    // each, 8 per word
+    constexpr int kPosWords = (EPL + 7) / 8;
     const uint32_t lane = lane_id();
     const bool valid = lane < nvalid;
     const uint32_t e = b + len;
@@ -427,7 +443,7 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
         // readable at every position (Sum/Min/Max: in LDS; Arg*: the element
         // positions in pos, the values still in LDS)
         A lane_acc;
-        PosBits pos = 0;
+        uint32_t pos[kPosWords] = {};
         if constexpr (!Acc::kArg) {
             T run = x[0];
 #pragma unroll
@@ -446,7 +462,7 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
                 const bool take = ((hmask >> j) & 1u) || better;
                 av = take ? x[j] : av;
                 ap = take ? (uint32_t)j : ap;
-                pos |= (PosBits)ap << (4 * j);
+                pos[j / 8] |= ap << (4 * (j % 8));
             }
             lane_acc = A{av, p0 + ap};
         }
@@ -454,7 +470,8 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
             if constexpr (!Acc::kArg) {
                 return stage[lane * (EPL + 1) + t];
             } else {
-                const uint32_t pt = (uint32_t)(pos >> (4 * t)) & 15u;
+                const uint32_t pw = kPosWords > 1 && t >= 8 ? pos[kPosWords - 1] : pos[0];
+                const uint32_t pt = (pw >> (4 * (t & 7))) & 15u;
                 return A{stage[lane * (EPL + 1) + pt], p0 + pt};
             }
         };
@@ -495,11 +512,11 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
         flat_seg_scan<Acc>(f, inc);
         const int fprev = wave_shr1((int)f, 0);
         const A iprev = Acc::template dpp_mv<kDppWaveShr1, 0xF>(inc, Acc::identity());
-        const A open = lane == 0 ? carry : (fprev ? iprev : Acc::combine(carry, iprev));
-        if (has_first) emit(first_sid, Acc::combine(open, first_acc));
+        const A open = lane == 0 ? carry : (fprev ? iprev : Acc::combine_ordered(carry, iprev));
+        if (has_first) emit(first_sid, Acc::combine_ordered(open, first_acc));
         const bool f63 = __builtin_amdgcn_readlane((int)f, kWave - 1) != 0;
         const A i63 = Acc::readlane_acc(inc, kWave - 1);
-        carry = f63 ? i63 : Acc::combine(carry, i63);
+        carry = f63 ? i63 : Acc::combine_ordered(carry, i63);
     }
 }
 
