@@ -451,3 +451,64 @@ def test_segments_at_the_top_of_the_32_bit_range(gpu):
             assert v[s_] == 1 and i[s_] == L[s_] - 1  # ties: the largest index
     del d
     torch.cuda.empty_cache()
+
+
+def _mixed_layout(rng, n):
+    """Blocks of whole waves (64 segments), each of one kind: tiling, gapped,
+    permuted, overlapping, long (> 8192) or empty segments, over [0, n)."""
+    bs, es = [], []
+    kinds = ["tiling", "gaps", "permuted", "overlap", "long", "empty"]
+    pos = 0
+    for _ in range(int(rng.integers(6, 14))):
+        kind = kinds[int(rng.integers(0, len(kinds)))]
+        m = 64 * int(rng.integers(1, 4)) - int(rng.integers(0, 2)) * int(rng.integers(1, 63))  # >= 2
+        if kind == "long":
+            L = rng.integers(8193, 20000, m)
+        elif kind == "empty":
+            L = np.zeros(m, np.int64)
+        else:
+            L = rng.geometric(1 / 60, m) - 1
+        if kind in ("tiling", "permuted", "long", "empty"):
+            e = pos + np.cumsum(L)
+            b = e - L
+        elif kind == "gaps":
+            g = rng.integers(0, 30, m) * (rng.random(m) < 0.5)
+            e = pos + np.cumsum(L + g)
+            b = e - L
+        else:  # overlapping: begins every 20 elements
+            b = pos + np.arange(m, dtype=np.int64) * 20
+            e = b + L
+        if kind == "permuted":
+            p = rng.permutation(m)
+            b, e = b[p], e[p]
+        if int(e.max()) > n or int(b.max()) > n:
+            continue  # does not fit: try another block
+        pos = int(max(e.max(), b.max()))
+        bs.append(b)
+        es.append(e)
+    if not bs:
+        e = np.cumsum(rng.geometric(1 / 60, 64) - 1)
+        bs, es = [e - (e - np.concatenate([[0], e[:-1]]))], [e]
+    return np.concatenate(bs).astype(np.uint32), np.concatenate(es).astype(np.uint32)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_mixed_layouts_random(gpu, seed):
+    """Random mixes of layouts in one launch (waves of different paths side by
+    side, ragged last wave), every op, against the oracle."""
+    import gpu_util as g
+
+    rng = np.random.default_rng(9000 + seed)
+    dtype = [np.int32, np.float32, np.int64, np.float64, np.uint32, np.uint64][seed % 6]
+    n = 1_500_000
+    b, e = _mixed_layout(rng, n)
+    a = rng.integers(0, 50, n).astype(dtype)  # ties; exact float sums
+    d = g.to_dev(a, pad=seed % 2)
+    S = b.size
+    log(f"segment mixed layouts seed={seed} S={S} {np.dtype(dtype).name}")
+    for method, op in (("Sum", o.OP_SUM), ("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        assert same(seg_call(method, d, S, (b, e), dtype), o.segment_reduce(op, a, b, e)), method
+    for method, is_max in (("ArgMin", False), ("ArgMax", True)):
+        v, i = seg_call(method, d, S, (b, e), dtype, arg=True)
+        ev, ei = o.segment_reduce_arg(is_max, a, b, e)
+        assert same(v, ev) and (i == ei).all(), method
