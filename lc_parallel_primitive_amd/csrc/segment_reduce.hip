@@ -229,9 +229,10 @@ __device__ __forceinline__ void wg_reduce_segment(const T *__restrict__ in, T *_
 // (begin[s + 1] >= end[s]: CSR offsets that tile one range, or ranges with
 // gaps between them that hold fewer elements than the segments do) streams
 // the range [B, E) from its first begin to its last end in chunks with
-// coalesced 16-byte loads instead of walking its segments 8 at a time (24
-// dependent load round trips per wave for mean length 128).  Each chunk goes
-// through LDS so that lane l then holds EPL consecutive elements p0 .. p0 +
+// coalesced 16-byte loads, whatever the lengths of its segments (reading
+// each segment on its own, with one 64-lane load per segment and step, took
+// 24 dependent load round trips per wave for mean length 128).  Each chunk
+// goes through LDS so that lane l then holds EPL consecutive elements p0 .. p0 +
 // EPL - 1.  The lane folds them in order, restarting at every segment begin
 // inside it, and the fold at a segment's last element is that segment's
 // result when the segment began inside the lane.  The one segment that began
@@ -306,8 +307,9 @@ __device__ __forceinline__ bool flat_eligible(uint32_t nvalid, uint32_t b, uint3
 // every element the wave reads).  Chunks are gathered with one load per
 // element, 64 consecutive virtual elements per wave load (one or two runs of
 // addresses); the fold runs on virtual indices, so Arg* positions relative
-// to a segment's begin are the same.  write_empty: whether a zero-length lane is an empty
-// segment to write (long segments, left to the workgroup path, are not).
+// to a segment's begin are the same.  write_empty: whether a zero-length
+// lane is an empty segment to write (long segments, left to the workgroup
+// path, are not).
 template <class T, int OP, bool GATHER>
 __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__restrict__ out,
                                               uint32_t *__restrict__ index_out, T init, uint64_t wseg0,
