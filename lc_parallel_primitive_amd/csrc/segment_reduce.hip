@@ -55,7 +55,9 @@ constexpr int kSegWaves = kSegBlock / kWave;
 // 113-124; the contiguous flat path 94 (a copy of it that only sums each
 // wave's range, with no segment logic, runs in 87.5): per-element branches
 // 105, branch-free fold 99, segment of each lane's first element by a
-// binary search in LDS 99 against a slot histogram and a DPP scan 97.  Arg*
+// binary search in LDS 99 against a slot histogram and a DPP scan 97, begin
+// and end bitmaps of each chunk (no LDS walks) 95 -> 93 (the same 2-3 %
+// for every op and layout).  Arg*
 // on the flat path: per-element branches 166-173, branch-free fold with the
 // arg positions packed in registers 111, combining in element order (one
 // empty check, no index tie break) 104.  The same segments in a random
@@ -253,9 +255,12 @@ constexpr int flat_epl()
 constexpr uint32_t kFlatMaxEnd = 0xFFFFFFFFu - 2u * kWave * 16u;
 template <class T>
 struct FlatSmem {
-    uint32_t bnd[kSegWaves][kSegPerWave + 1];   // begins (~0 past the wave's segments)
-    uint32_t ends[kSegWaves][kSegPerWave + 1];  // begin + length (~0 past them)
-    uint32_t slots[kSegWaves][kWave];
+    uint32_t bnd[kSegWaves][kSegPerWave];     // begins
+    uint32_t seg_of[kSegWaves][kSegPerWave];  // the r-th non-empty segment
+    // bitmaps of a chunk (one bit per element): non-empty segment begins, and
+    // their last elements
+    uint32_t bbits[kSegWaves][kWave * flat_epl<T>() / 32];
+    uint32_t ebits[kSegWaves][kWave * flat_epl<T>() / 32];
     T stage[kSegWaves][kWave * (flat_epl<T>() + 1)];  // +1: conflict-free column reads
     // gather: bitmap of the segment ends inside a chunk, one bit per virtual
     // element, and the element-index offset of each non-empty segment
@@ -315,8 +320,8 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
                                               uint32_t *__restrict__ index_out, T init, uint64_t wseg0,
                                               uint32_t nvalid, uint32_t b, uint32_t len, bool write_empty,
                                               uint32_t delta, uint32_t g_lo, uint32_t g_bytes, uint32_t *bnd,
-                                              uint32_t *ends, uint32_t *slots, T *stage, uint32_t *gbits,
-                                              uint32_t *gdelta)
+                                              uint32_t *seg_of, uint32_t *bbits, uint32_t *ebits, T *stage,
+                                              uint32_t *gbits, uint32_t *gdelta)
 {
     using Acc = SegAcc<T, OP>;
     using A = typename Acc::A;
@@ -332,11 +337,15 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
     const uint32_t e = b + len;
     const uint32_t B = (uint32_t)__builtin_amdgcn_readfirstlane((int)b);
     const uint32_t E = (uint32_t)__builtin_amdgcn_readlane((int)e, (int)nvalid - 1);
-    bnd[lane] = valid ? b : ~0u;
-    ends[lane] = valid ? e : ~0u;
-    if (lane == 0) {
-        bnd[kSegPerWave] = ~0u;
-        ends[kSegPerWave] = ~0u;
+    // segments in order of their ends: the non-empty ones get ranks (their
+    // ends are distinct and increasing), seg_of maps a rank to its segment
+    const bool nonempty = valid && len > 0;
+    const uint64_t ne_mask = ballot(nonempty);
+    const uint32_t ne_rank = (uint32_t)__builtin_popcountll(ne_mask & ((1ull << lane) - 1));
+    bnd[lane] = b;
+    if (nonempty) {
+        seg_of[ne_rank] = lane;
+        if constexpr (GATHER) gdelta[ne_rank] = delta;
     }
     __builtin_amdgcn_wave_barrier();
     if (valid && len == 0 && write_empty) seg_store<T, OP>(Acc::identity(), b, init, out, index_out, wseg0 + lane);
@@ -358,12 +367,7 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
     // they only reach folds that never become results.
     u32x4 v[GATHER ? 1 : LOADS];
     T g[GATHER ? EPL : 1];
-    const bool nonempty = valid && len > 0;
     const uint32_t gend = nonempty ? e : 0u;  // non-empty ends are distinct and >= 1
-    if constexpr (GATHER) {
-        const uint64_t ne = ballot(nonempty);
-        if (nonempty) gdelta[__builtin_popcountll(ne & ((1ull << lane) - 1))] = delta;
-    }
     auto load_chunk = [&](uint32_t c) {
         if constexpr (GATHER) {
             const uint32_t cb = c * CH;
@@ -418,29 +422,28 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
         for (int j = 0; j < EPL; ++j) x[j] = stage[lane * (EPL + 1) + j];
         __builtin_amdgcn_wave_barrier();
 
-        // i0 = the segments that end at or before p0 (ends are sorted), from a
-        // 64-entry histogram of the lanes whose first element follows each
-        // end, those below the chunk counted by one ballot
+        // the chunk's begins and last elements as bitmaps: a lane's EPL bits are
+        // its restarts (hmask) and the segments it completes (emask); the rank
+        // of its first completed segment counts the ends before it
         const uint32_t p0 = base + lane * EPL;
-        const uint32_t lim = p0 >= E ? E : (E - p0 < (uint32_t)EPL ? E : p0 + EPL);
-        const uint32_t below = (uint32_t)__builtin_popcountll(ballot(valid && e < base));
-        slots[lane] = 0;
-        __builtin_amdgcn_wave_barrier();
-        const uint32_t d = e - base;
-        if (valid && e >= base && d <= (uint32_t)(kWave - 1) * EPL) atomicAdd(&slots[(d + EPL - 1) / EPL], 1u);
-        __builtin_amdgcn_wave_barrier();
-        const uint32_t i0 = below + wave_inclusive_scan(slots[lane], SumOp());
-        // bit t of hmask: a segment begins at p0 + t (only segment i0 can
-        // have begun before p0; every later one begins after its end > p0)
-        uint32_t hmask = 0;
-        {
-            uint32_t i = i0, q = bnd[i];
-            if (q < p0) q = bnd[++i];
-            while (q < lim) {
-                hmask |= 1u << (q - p0);
-                q = bnd[++i];
-            }
+        if (lane < CH / 32) {
+            bbits[lane] = 0;
+            ebits[lane] = 0;
         }
+        __builtin_amdgcn_wave_barrier();
+        {
+            const uint32_t tb = b - base, te = e - 1u - base;  // past the chunk or below it: >= CH
+            if (nonempty && tb < CH) atomicOr(&bbits[tb / 32], 1u << (tb % 32));
+            if (nonempty && te < CH) atomicOr(&ebits[te / 32], 1u << (te % 32));
+        }
+        __builtin_amdgcn_wave_barrier();
+        constexpr uint32_t kLaneBits = EPL >= 32 ? ~0u : (1u << EPL) - 1u;
+        const uint32_t bw = lane * EPL / 32, bsh = lane * EPL % 32;
+        const uint32_t hmask = (bbits[bw] >> bsh) & kLaneBits;
+        const uint32_t emask = (ebits[bw] >> bsh) & kLaneBits;
+        const uint32_t below = (uint32_t)__builtin_popcountll(ballot(nonempty && e <= base));
+        const uint32_t ecount = (uint32_t)__builtin_popcount(emask);
+        const uint32_t rank0 = below + wave_inclusive_scan(ecount, SumOp()) - ecount;
         // in-order fold with restarts; the lane's own prefix folds stay
         // readable at every position (Sum/Min/Max: in LDS; Arg*: the element
         // positions in pos, the values still in LDS)
@@ -477,9 +480,8 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
                 return A{stage[lane * (EPL + 1) + pt], p0 + pt};
             }
         };
-        // segments ending inside the lane (last element in [p0, lim))
-        const uint32_t e0 = ends[i0];
-        const bool has_end = e0 <= lim;
+        // segments ending inside the lane
+        const bool has_end = emask != 0;
         if constexpr (!Acc::kArg) {
             if (ballot(has_end)) {
 #pragma unroll
@@ -491,21 +493,22 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
         uint32_t first_sid = 0;
         A first_acc = Acc::identity();
         if (has_end) {
-            uint32_t i = i0, ee = e0;
-            do {
-                const uint32_t bi = bnd[i];
-                if (ee > bi) {  // empty segments were written at the start
-                    const A val = prefix_at(ee - 1 - p0);
-                    if (bi < p0) {
-                        has_first = true;
-                        first_sid = i;
-                        first_acc = val;
-                    } else {
-                        emit(i, val);
-                    }
-                }
-                ee = ends[++i];
-            } while (ee <= lim);
+            // the first completed segment began before p0 when no begin bit
+            // precedes its last element (a later segment begins after it ends)
+            uint32_t m = emask, rk = rank0;
+            const uint32_t k0 = (uint32_t)__builtin_ctz(m);
+            if ((hmask & ((2u << k0) - 1u)) == 0) {
+                has_first = true;
+                first_sid = seg_of[rk];
+                first_acc = prefix_at(k0);
+                m &= m - 1;
+                ++rk;
+            }
+            while (m) {
+                emit(seg_of[rk], prefix_at((uint32_t)__builtin_ctz(m)));
+                m &= m - 1;
+                ++rk;
+            }
         }
         __builtin_amdgcn_wave_barrier();  // LDS reads done before the next chunk's stage writes
         // open segment at each lane's start: carry, then the lanes before
@@ -574,8 +577,8 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__re
     const uint32_t nvalid = wseg0 < S ? (uint32_t)(S - wseg0 < kSegPerWave ? S - wseg0 : kSegPerWave) : 0u;
     if (vec_ok && flat_eligible<T>(nvalid, b, len)) {
         flat_segments<T, OP, false>(in, out, index_out, init, wseg0, nvalid, b, len, true, 0u, 0u, 0u,
-                                    s_flat.bnd[wave], s_flat.ends[wave], s_flat.slots[wave], s_flat.stage[wave],
-                                    s_flat.gbits[wave], s_flat.gdelta[wave]);
+                                    s_flat.bnd[wave], s_flat.seg_of[wave], s_flat.bbits[wave], s_flat.ebits[wave],
+                                    s_flat.stage[wave], s_flat.gbits[wave], s_flat.gdelta[wave]);
     } else if (nvalid > 0) {
         const uint32_t vlen = is_long ? 0u : len;
         // elements the gather reads: [lo, hi), at most 4 GiB for one buffer resource
@@ -586,8 +589,9 @@ __global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__re
         if (bytes <= 0xFFFFFFFFull) {
             const uint32_t vb = wave_inclusive_scan(vlen, SumOp()) - vlen;  // <= 64 * kSegLong
             flat_segments<T, OP, true>(in, out, index_out, init, wseg0, nvalid, vb, vlen, !is_long, b - lo - vb, lo,
-                                       (uint32_t)bytes, s_flat.bnd[wave], s_flat.ends[wave], s_flat.slots[wave],
-                                       s_flat.stage[wave], s_flat.gbits[wave], s_flat.gdelta[wave]);
+                                       (uint32_t)bytes, s_flat.bnd[wave], s_flat.seg_of[wave], s_flat.bbits[wave],
+                                       s_flat.ebits[wave], s_flat.stage[wave], s_flat.gbits[wave],
+                                       s_flat.gdelta[wave]);
         } else {
             wave_segments<T, OP>(in, out, index_out, init, wseg0, nvalid, b, len);
         }
