@@ -73,7 +73,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only: every box has a single MI355X; "
-                                   "run with --gpus 1 (the multi-GPU sharding is described in DESIGN.md)"}))
+                                   "run with --gpus 1 (sharding across GPUs is designed, not built)"}))
         sys.exit(2)
 
     import torch
