@@ -170,6 +170,26 @@ def test_pairs_descending_stable_vs_oracle(gpu, kdt, vdt, n):
     assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("descending", [False, True])
+@pytest.mark.parametrize("n", [4097, 100_003])
+def test_special_float_keys_vs_oracle(gpu, dtype, descending, n):
+    # NaNs of both signs and several payloads, +-inf, subnormals, +-0: the
+    # order is fixed by bit patterns (the oracle is pinned against an IEEE
+    # total order built without the key twiddle)
+    import gpu_util as g
+    from conftest import special_float_keys
+
+    a = special_float_keys(dtype, n, seed=n + 7)
+    v = np.arange(n, dtype=np.uint32)
+    log(f"sort special floats {np.dtype(dtype).name} n={n} descending={descending}")
+    got = g.to_host(sort_keys(g.to_dev(a), n, dtype, descending=descending))
+    assert same_bits(got, o.radix_sort(a, descending=descending))
+    ko, vo = sort_pairs(g.to_dev(a), g.to_dev(v), n, dtype, np.uint32, descending=descending)
+    rk, rv = o.radix_sort(a, v, descending=descending)
+    assert same_bits(g.to_host(ko), rk) and same_bits(g.to_host(vo), rv)
+
+
 def test_low_entropy_keys(gpu):
     import gpu_util as g
     from lc_parallel_primitive_amd import datagen

@@ -309,6 +309,48 @@ def test_sort_keys_descending_vs_numpy(dt):
         assert (np.signbit(a[a == 0]) == np.signbit(got[got == 0])).all()
 
 
+def float_total_order_perm(a: np.ndarray, descending: bool = False) -> np.ndarray:
+    """Permutation that orders float keys as an IEEE-754 radix sort does, built
+    from value comparisons and NaN signs and bit patterns only (not from the
+    key twiddle): negative NaNs (larger bit patterns first), then every other
+    value in numeric order with -0.0 == +0.0, then positive NaNs (smaller bit
+    patterns first); equal keys in input order.  Descending reverses the
+    order of distinct keys and keeps equal keys in input order."""
+    bits = a.view(np.uint32 if a.dtype.itemsize == 4 else np.uint64)
+    idx = np.arange(a.size)
+    nan = np.isnan(a)
+    neg = np.signbit(a)
+    negnan, posnan, num = idx[nan & neg], idx[nan & ~neg], idx[~nan]
+    up = lambda ix, key: ix[np.argsort(key[ix], kind="stable")]
+    down = lambda ix, key: ix[stable_descending_perm(key[ix])]
+    if descending:
+        return np.concatenate([down(posnan, bits), down(num, a), up(negnan, bits)])
+    return np.concatenate([down(negnan, bits), up(num, a), up(posnan, bits)])
+
+
+def test_float_total_order_perm_small_case():
+    f = np.float32
+    nan = lambda b: np.array([b], np.uint32).view(f)[0]
+    a = np.array([1.0, nan(0x7FC00001), -0.0, -np.inf, nan(0xFFC00000), 0.0, np.inf, nan(0x7FC00000),
+                  nan(0xFFC00001), -2.5, 1.0], f)
+    assert float_total_order_perm(a).tolist() == [8, 4, 3, 9, 2, 5, 0, 10, 6, 7, 1]
+    assert float_total_order_perm(a, descending=True).tolist() == [1, 7, 6, 0, 10, 2, 5, 9, 3, 4, 8]
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("descending", [False, True])
+def test_sort_special_floats_vs_total_order(dt, descending):
+    from conftest import special_float_keys
+
+    a = special_float_keys(dt, 60_001, seed=21)
+    perm = float_total_order_perm(a, descending)
+    v = np.arange(a.size, dtype=np.uint32)
+    ko = o.radix_sort(a, descending=descending, nthreads=3, tile_items=1024)
+    ko2, vo = o.radix_sort(a, v, descending=descending, nthreads=3, tile_items=1024)
+    assert ko.tobytes() == a[perm].tobytes()  # bit-exact: NaN payloads, -0.0 / +0.0 order
+    assert ko2.tobytes() == a[perm].tobytes() and (vo == perm).all()
+
+
 def test_stable_descending_perm_is_independent_of_the_oracle():
     a = np.array([3, 1, 3, 2, 1, 3], dtype=np.uint32)
     assert stable_descending_perm(a).tolist() == [0, 2, 5, 3, 1, 4]
