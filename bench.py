@@ -14,8 +14,8 @@ measured live with HIP events recorded by the library on the launch stream;
 8 digit passes moving data, the by-key primitives, segment reduce), each with
 its dominant kernel's time and, where BASELINE names one, a CPU number;
 `cpu_baseline` and those per-entry CPU numbers time the oracle's C
-restatements of the reference algorithms (oracle/) on bounded samples on
-this host's cores.
+restatements of the reference algorithms (oracle/) at each configuration's
+full size on this host's cores.
 """
 from __future__ import annotations
 
@@ -254,7 +254,7 @@ def main():
             add("DeviceReduce::Sum int32 N=2^28", 4 * n + 4,
                 lambda: chk(L.lcpp_reduce_sum(I32, ctypes.c_void_p(t1.data_ptr()), tb, ctypes.c_void_p(x.data_ptr()),
                                               ctypes.c_void_p(o1.data_ptr()), n, sp), "reduce"), 20, "reduce_partials",
-                cpu=lambda: cpu_reduce(1 << 26))
+                cpu=lambda: cpu_reduce(n))
             n24 = 1 << 24
             add("DeviceReduce::Sum int32 N=2^24 (configs[0])", 4 * n24 + 4,
                 lambda: chk(L.lcpp_reduce_sum(I32, ctypes.c_void_p(t1.data_ptr()), tb, ctypes.c_void_p(x.data_ptr()),
@@ -278,7 +278,7 @@ def main():
                 lambda: chk(L.lcpp_scan_exclusive_sum(U32, ctypes.c_void_p(t1.data_ptr()), tb,
                                                       ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
                                                       n, sp), "scan"), 20, "scan_exclusive",
-                cpu=lambda: cpu_scan("u8_u32", False, 1 << 26))
+                cpu=lambda: cpu_scan("u8_u32", False, n))
             del x
             xf = datagen.normal_f32(n)
             yf = torch.empty_like(xf)
@@ -286,7 +286,7 @@ def main():
                 lambda: chk(L.lcpp_scan_inclusive_sum(F32, ctypes.c_void_p(t1.data_ptr()), tb,
                                                       ctypes.c_void_p(xf.data_ptr()), ctypes.c_void_p(yf.data_ptr()),
                                                       n, sp), "scan"), 20, "scan_inclusive",
-                cpu=lambda: cpu_scan("normal_f32", True, 1 << 26))
+                cpu=lambda: cpu_scan("normal_f32", True, n))
             del xf, yf, y, t1
         if want("sort_and3"):
             n = 1 << 28
@@ -298,7 +298,7 @@ def main():
                 lambda: chk(L.lcpp_radix_sort_keys(U32, ctypes.c_void_p(t1.data_ptr()), tb,
                                                    ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(ko.data_ptr()), n,
                                                    sp), "sort"), 10, "rs_onesweep", items=n,
-                cpu=lambda: cpu_sort("keys_u32_and3", 1 << 25))
+                cpu=lambda: cpu_sort("keys_u32_and3", n))
             del k, ko, t1
         if want("pairs"):
             n = 1 << 27
@@ -325,7 +325,7 @@ def main():
                     # histogram (8 B) plus the two passes that move data (2 x 24 B)
                     add("DeviceRadixSort::SortPairs uint64->uint32 N=2^27 (configs[3]: 16 random low bits; "
                         "2 of 8 digit passes move data)", 56 * n, call, 5, "rs_onesweep", items=n,
-                        cpu=lambda: cpu_pairs(1 << 24),
+                        cpu=lambda: cpu_pairs(n),
                         note="56 B per pair counted: the 6 passes whose digit every key shares are skipped; "
                              "the full-range entry times 8 moving passes")
                 del k, ko
@@ -390,7 +390,7 @@ def main():
 
     # ------------------------------------------------------------ CPU baseline (oracle onesweep port)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_sort("keys_u32", 1 << 25, seed=0xC3A)
+        result["cpu_baseline"] = cpu_sort("keys_u32", 1 << 28, seed=0xC3A)
         progress(f"cpu baseline: {result['cpu_baseline']['value']} Gkeys/s")
 
     print(json.dumps(result), flush=True)
@@ -400,8 +400,9 @@ def main():
 # The reference's own CPU path (LuisaCompute's fallback backend) cannot be built:
 # LuisaCompute is not vendored and the reference's CMake disables that backend.
 # These time the oracle's C restatements of the reference algorithms (same tile
-# decomposition, look-back across threads) on this host, on bounded samples of
-# each configuration; median of 3 after 1 warm-up.
+# decomposition, look-back across threads) on this host, on each configuration
+# at its full size (a 2^28-key sort is ~1.6 s on 16 threads of the GPU box's
+# host); median of 3 after 1 warm-up.
 
 def _threads():
     return max(1, min(len(os.sched_getaffinity(0)), 16))  # the GPU box's CPU share is 16 threads
