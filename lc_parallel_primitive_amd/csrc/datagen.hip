@@ -12,6 +12,8 @@
 
 #include <vector>
 
+#include "by_key.hpp"  // the wave64 primitives under test (common.hpp, wave_seg_scan)
+
 namespace {
 
 constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
@@ -287,6 +289,55 @@ void shape_onesweep_tile(const uint32_t *__restrict__ in, uint32_t *__restrict__
     }
 }
 
+// Known-answer kernel for the shared wave64 primitives the product kernels
+// are built from (common.hpp, by_key.hpp), over int32 data: lane l of wave w
+// holds element w * 64 + l; n is a multiple of 64, so every wave is either
+// wholly in range or exits whole (the DPP and ballot steps see full waves).
+//   0  out[w] = wave_allreduce(x, Sum)        (the wave's lane 0 writes)
+//   1  out[i] = wave_inclusive_scan(x, Sum) - x (exclusive sum)
+//   2  out[i] = wave_inclusive_scan(x, Sum)
+//   3  out[i] = sum since the last lane <= i whose flag is set, or since
+//      lane 0 (wave_seg_scan of (flag, x) pairs)
+//   4  out[i] = mask_rank(ballot(flag != 0)): flagged lanes below lane i
+//   5  out[i] = wave_inclusive_scan(x, Max)
+//   6  out[w] = wave_allreduce(x, Min)
+//   7  out[i] = wave_shr1(x, fill = -1): x of lane i - 1
+// Sums wrap (two's complement), as the primitives' integer sums do.
+__global__ __launch_bounds__(256) void wave_kat_kernel(const int32_t *__restrict__ in,
+                                                       const int32_t *__restrict__ flags, int32_t *__restrict__ out,
+                                                       uint32_t n, int kind)
+{
+    using namespace lcpp;
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const int32_t x = in[i];
+    const uint32_t lane = lane_id();
+    switch (kind) {
+    case 0: {
+        const int32_t r = wave_allreduce(x, SumOp());
+        if (lane == 0) out[i / kWave] = r;
+        break;
+    }
+    case 1: out[i] = wave_inclusive_scan(x, SumOp()) - x; break;
+    case 2: out[i] = wave_inclusive_scan(x, SumOp()); break;
+    case 3: {
+        bool f = flags[i] != 0;
+        int32_t v = x;
+        wave_seg_scan(f, v, SumOp());
+        out[i] = v;
+        break;
+    }
+    case 4: out[i] = (int32_t)mask_rank(ballot(flags[i] != 0)); break;
+    case 5: out[i] = wave_inclusive_scan(x, MaxOp()); break;
+    case 6: {
+        const int32_t r = wave_allreduce(x, MinOp());
+        if (lane == 0) out[i / kWave] = r;
+        break;
+    }
+    default: out[i] = wave_shr1(x, -1); break;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -348,6 +399,19 @@ int lcpp_dg_lds_order_probe(uint64_t seed, uint32_t pattern, uint32_t waves, uin
     if (!violations || pattern > 3 || waves == 0 || (waves & 3)) return -1;
     lds_order_probe_kernel<<<waves / 4, 256, 0, static_cast<hipStream_t>(stream)>>>(
         seed, pattern, rounds, static_cast<unsigned long long *>(violations));
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// One of the wave64 known-answer cases above (kind 0..7) over n int32
+// elements, n a multiple of 64; `flags` is read by kinds 3 and 4 only.
+// out holds n / 64 elements for kinds 0 and 6, n otherwise.
+int lcpp_dg_wave_kat(int kind, const void *in, const void *flags, void *out, uint64_t n, void *stream)
+{
+    if (kind < 0 || kind > 7 || !in || !out || n == 0 || (n % 64) || n > 0x7FFFFFFFull) return -1;
+    if ((kind == 3 || kind == 4) && !flags) return -1;
+    wave_kat_kernel<<<(uint32_t)((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const int32_t *>(in), static_cast<const int32_t *>(flags), static_cast<int32_t *>(out),
+        (uint32_t)n, kind);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

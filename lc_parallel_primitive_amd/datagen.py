@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.lcpp_dg_check_stable_pairs_u32.argtypes = [vp, vp, vp, u64, vp, vp]
         L.lcpp_dg_lds_order_probe.restype = i
         L.lcpp_dg_lds_order_probe.argtypes = [u64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp, vp]
+        L.lcpp_dg_wave_kat.restype = i
+        L.lcpp_dg_wave_kat.argtypes = [ctypes.c_int, vp, vp, vp, u64, vp]
         _lib = L
     return _lib
 
@@ -270,3 +272,22 @@ def lds_order_probe(seed: int, pattern: int, waves: int, rounds: int) -> int:
     _run(lib().lcpp_dg_lds_order_probe(seed, pattern, waves, rounds, ctypes.c_void_p(v.data_ptr()), _stream()),
          "lds_order_probe")
     return int(v.cpu().view(torch.int64).item())
+
+
+WAVE_KAT_KINDS = {"reduce_sum": 0, "exclusive_sum": 1, "inclusive_sum": 2, "segmented_sum": 3, "flag_rank": 4,
+                  "inclusive_max": 5, "reduce_min": 6, "shift_up": 7}
+
+
+def wave_kat(kind: str, x, flags=None):
+    """One of the wave64 primitive cases of datagen.hip's wave_kat_kernel over
+    int32 device tensor x (length a multiple of 64); returns the device output
+    (one value per wave for the reductions, one per element otherwise)."""
+    import torch
+
+    k = WAVE_KAT_KINDS[kind]
+    n = x.numel()
+    out = torch.empty(n // 64 if k in (0, 6) else n, dtype=torch.int32, device=x.device)
+    fp = ctypes.c_void_p(flags.data_ptr()) if flags is not None else None
+    _run(lib().lcpp_dg_wave_kat(k, ctypes.c_void_p(x.data_ptr()), fp, ctypes.c_void_p(out.data_ptr()), n,
+                                _stream()), f"wave_kat {kind}")
+    return out
