@@ -148,7 +148,11 @@ def test_scan_by_key_ops_and_init(gpu, op, vdt):
 
 
 def test_scan_by_key_one_run_and_distinct_keys(gpu):
-    n = 1_000_003  # one run spanning ~120 tiles: every tile waits on the look-back
+    # one run spanning ~120 tiles: every tile waits on the segmented (key,
+    # value) look-back; decoupled_look_back.cpp:176-300 checks the same
+    # combine over tiles that all share one key (exclusive prefix = the sum
+    # of the tiles before)
+    n = 1_000_003
     v = values(np.int32, n, 5)
     one = np.full(n, 3, np.uint32)
     for inclusive in (False, True):
