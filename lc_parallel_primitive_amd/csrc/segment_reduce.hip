@@ -385,7 +385,17 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
                 const uint32_t rk = __builtin_amdgcn_mbcnt_hi(whi, __builtin_amdgcn_mbcnt_lo(wlo, rank));
                 rank += (uint32_t)__builtin_popcount(wlo) + (uint32_t)__builtin_popcount(whi);
                 const uint32_t dl = gdelta[rk < kSegPerWave ? rk : kSegPerWave - 1];
-                g[j] = buf_ld_elem_nt<T>(r, (cb + (uint32_t)j * kWave + lane + dl) * (uint32_t)sizeof(T));
+                // The byte offset of a segment's element is non-negative, but
+                // its lane part (lane + dl) is not: left to itself the compiler
+                // moves j * 64 (and cb) into the load's immediate / SGPR offset
+                // and passes the lane part as the VGPR offset, wrapped below
+                // zero.  The hardware does not add those two modulo 2^32: such
+                // loads returned wrong data (a random-order layout where a
+                // wave's lowest-addressed segment sat in its second 64-element
+                // window).  The opaque copy keeps the whole offset in the VGPR.
+                uint32_t off = (cb + (uint32_t)j * kWave + lane + dl) * (uint32_t)sizeof(T);
+                asm volatile("" : "+v"(off));
+                g[j] = buf_ld_elem_nt<T>(r, off);
             }
         } else {
 #pragma unroll

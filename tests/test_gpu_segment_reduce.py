@@ -381,6 +381,59 @@ def test_nontiling_full_size_permuted(gpu):
     assert same(v, ev) and (i == ei).all()
 
 
+@pytest.mark.parametrize("layout", ["reversed_waves", "random_tiny"])
+def test_gather_lowest_segment_late_in_wave(gpu, layout):
+    """Gather waves whose lowest-addressed segments sit late in the wave's
+    virtual range, so an element's byte offset from the wave's lowest
+    begin is smaller than its position in the gathered order: every wave of
+    "reversed_waves" (64 segments of 1-3 elements laid out in descending
+    address order, 2^22 segments), and the layout that exposed a load whose
+    offset had been split between a wrapped VGPR part and an immediate
+    (tiling segments of mean length ~1.4 in a random order, the values one
+    constant).  Every op, exact against the oracle, the output's guard
+    region untouched."""
+    import torch
+
+    import gpu_util as g
+
+    rng = np.random.default_rng(17 if layout == "reversed_waves" else 23)
+    if layout == "reversed_waves":
+        S = 1 << 22
+        lens = rng.integers(1, 4, size=S).astype(np.int64)
+        w = lens.reshape(-1, 64)
+        # within each wave, lane k's segment lies after lane k + 1's
+        starts = np.cumsum(w[:, ::-1], axis=1) - w[:, ::-1]
+        wave_base = np.concatenate([[0], np.cumsum(w.sum(axis=1))[:-1]])
+        b = (wave_base[:, None] + starts[:, ::-1]).ravel()
+        e = b + lens
+        n = int(e.max())
+        a = rng.integers(-(1 << 30), 1 << 30, size=n, dtype=np.int32)
+    else:
+        n, S = 6_000_007, 4_200_011
+        cuts = np.sort(rng.integers(0, n + 1, size=S - 1))
+        bnd = np.concatenate([[0], cuts, [n]])
+        perm = rng.permutation(S)
+        b, e = bnd[:-1][perm], bnd[1:][perm]
+        a = np.full(n, -1201695826, dtype=np.int32)
+    b, e = b.astype(np.uint32), e.astype(np.uint32)
+    log(f"segment gather, lowest segment late: {layout} n={n} S={S}")
+    d, db, de = g.to_dev(a), g.to_dev(b), g.to_dev(e)
+    from lc_parallel_primitive_amd import DeviceSegmentReduce
+
+    r = DeviceSegmentReduce()
+    outg = torch.full((S + 1024,), 7, dtype=torch.int32, device="cuda")
+    idxg = torch.full((S + 1024,), 7, dtype=torch.int32, device="cuda")
+    out, idx = outg[:S], idxg[:S].view(torch.uint32)
+    for method, op in (("Sum", o.OP_SUM), ("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        getattr(r, method)(None, d, out, S, db, de)
+        assert (g.to_host(out) == o.segment_reduce(op, a, b, e)).all(), method
+    for method, is_max in (("ArgMin", False), ("ArgMax", True)):
+        getattr(r, method)(None, d, out, idx, S, db, de)
+        ev, ei = o.segment_reduce_arg(is_max, a, b, e)
+        assert (g.to_host(out) == ev).all() and (g.to_host(idx) == ei).all(), method
+    assert (g.to_host(outg[S:]) == 7).all() and (g.to_host(idxg[S:]) == 7).all()
+
+
 def test_segments_more_than_4gib_apart(gpu):
     """A wave whose segments lie more than 4 GiB apart (int32 input of 2^30 +
     2^20 elements, value = index) takes the one-segment-at-a-time path:
