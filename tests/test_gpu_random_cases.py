@@ -1,0 +1,150 @@
+"""Seeded randomized parity cases for every primitive: random sizes (1 to
+2^20, log-uniform), integer dtypes, value distributions (uniform, few
+distinct, AND-of-3, constant), sort directions, run lengths and segment
+layouts (tiling, random order, random windows with overlaps, gaps and
+inverted ranges).  Integer data, so every result is exact against the
+oracle.  A larger sweep of this kind (sizes to 2^25) found the gather load
+whose offset wrapped below zero (see test_gather_lowest_segment_late_in_wave)."""
+import numpy as np
+import pytest
+
+from conftest import log
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+INT_DTYPES = [np.int32, np.uint32, np.int64, np.uint64]
+
+
+def values(rng, dt, n, kind):
+    info = np.iinfo(dt)
+
+    def uni():
+        return rng.integers(info.min, info.max, size=n, dtype=dt, endpoint=True)
+
+    if kind == 0:
+        return uni()
+    if kind == 1:
+        return rng.integers(0, 7, size=n).astype(dt)
+    if kind == 2:
+        return uni() & uni() & uni()
+    return np.full(n, rng.integers(info.min, info.max, dtype=dt, endpoint=True), dtype=dt)
+
+
+def case_params(seed):
+    rng = np.random.default_rng(seed)
+    n = int(np.exp(rng.uniform(0, np.log(1 << 20))))
+    return rng, n, INT_DTYPES[rng.integers(0, 4)], int(rng.integers(0, 4))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_reduce_and_scan(gpu, seed):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce, DeviceScan
+
+    rng, n, dt, kind = case_params(1000 + seed)
+    a = values(rng, dt, n, kind)
+    log(f"random reduce/scan seed={seed} n={n} {np.dtype(dt).name} kind={kind}")
+    d = g.to_dev(a)
+    out = g.empty(1, dt)
+    r = DeviceReduce()
+    tmp = g.temp(DeviceReduce.GetTempStorageBytes(np.dtype(dt).name, n))
+    for nm, op in (("Sum", o.OP_SUM), ("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        getattr(r, nm)(tmp, d, out, n)
+        assert g.to_host(out)[0] == o.reduce(op, a), nm
+    idx = g.empty(1, np.uint32)
+    tmpa = g.temp(DeviceReduce.GetArgTempStorageBytes(np.dtype(dt).name, n))
+    for nm, is_max in (("ArgMin", False), ("ArgMax", True)):
+        getattr(r, nm)(tmpa, d, out, idx, n)
+        v, i = o.reduce_arg(is_max, a)
+        assert g.to_host(out)[0] == v and g.to_host(idx)[0] == i, nm
+    so = g.empty(n, dt)
+    s = DeviceScan()
+    tmps = g.temp(DeviceScan.GetTempStorageBytes(np.dtype(dt).name, n))
+    for inclusive in (False, True):
+        (s.InclusiveSum if inclusive else s.ExclusiveSum)(tmps, d, so, n)
+        assert (g.to_host(so) == o.scan(a, inclusive)).all(), inclusive
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_sorts(gpu, seed):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceRadixSort
+
+    rng, n, dt, kind = case_params(2000 + seed)
+    a = values(rng, dt, n, kind)
+    desc = bool(rng.integers(0, 2))
+    vdt = [np.uint32, np.uint64][rng.integers(0, 2)]
+    v = np.arange(n, dtype=vdt)
+    log(f"random sort seed={seed} n={n} {np.dtype(dt).name} kind={kind} desc={desc}")
+    s = DeviceRadixSort()
+    ko = g.empty(n, dt)
+    tmp = g.temp(DeviceRadixSort.GetSortKeysTempStorageBytes(np.dtype(dt).name, n))
+    (s.SortKeysDescending if desc else s.SortKeys)(tmp, g.to_dev(a), ko, n)
+    assert (g.to_host(ko) == o.radix_sort(a, descending=desc)).all()
+    vo = g.empty(n, vdt)
+    tmp = g.temp(DeviceRadixSort.GetSortPairsTempStorageBytes(np.dtype(dt).name, np.dtype(vdt).name, n))
+    (s.SortPairsDescending if desc else s.SortPairs)(tmp, g.to_dev(a), ko, g.to_dev(v), vo, n)
+    rk, rv = o.radix_sort(a, v, descending=desc)
+    assert (g.to_host(ko) == rk).all() and (g.to_host(vo) == rv).all()
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_by_key(gpu, seed):
+    import torch
+
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce, DeviceScan
+
+    rng, n, dt, kind = case_params(3000 + seed)
+    run = int(rng.integers(1, 400))
+    keys = np.repeat(rng.integers(0, 4, size=n // run + 1), run)[:n].astype(dt)
+    vals = values(rng, np.int32, n, 1)
+    op = ["sum", "min", "max"][rng.integers(0, 3)]
+    log(f"random by-key seed={seed} n={n} {np.dtype(dt).name} run={run} op={op}")
+    dk, dv = g.to_dev(keys), g.to_dev(vals)
+    s = DeviceScan()
+    so = g.empty(n, np.int32)
+    tmp = g.temp(DeviceScan.GetScanByKeyTempStorageBytes(np.dtype(dt).name, "int32", n))
+    for inclusive in (False, True):
+        (s.InclusiveSumByKey if inclusive else s.ExclusiveSumByKey)(tmp, dk, dv, so, n)
+        assert (g.to_host(so) == o.scan_by_key(keys, vals, inclusive)).all(), inclusive
+    uk, ag = g.empty(n, dt), g.empty(n, np.int32)
+    nr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tmp = g.temp(DeviceReduce.GetReduceByKeyTempStorageBytes(np.dtype(dt).name, "int32", n))
+    DeviceReduce().ReduceByKey(tmp, dk, dv, uk, ag, nr, op, n)
+    rk, rv = o.reduce_by_key(keys, vals, {"sum": o.OP_SUM, "min": o.OP_MIN, "max": o.OP_MAX}[op])
+    m = int(nr.item())
+    assert m == rk.size and (g.to_host(uk)[:m] == rk).all() and (g.to_host(ag)[:m] == rv).all()
+
+
+@pytest.mark.parametrize("seed", range(36))
+def test_random_segments(gpu, seed):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceSegmentReduce
+
+    rng, n, dt, kind = case_params(4000 + seed)
+    a = values(rng, dt, n, kind)
+    S = max(1, int(rng.integers(1, 1 + max(1, n // int(rng.integers(1, 200))))))
+    layout = seed % 3
+    if layout < 2:  # tiling, in order or in a random order
+        cuts = np.sort(rng.integers(0, n + 1, size=S - 1))
+        bnd = np.concatenate([[0], cuts, [n]]).astype(np.uint32)
+        b, e = bnd[:-1].copy(), bnd[1:].copy()
+        if layout == 1:
+            p = rng.permutation(S)
+            b, e = b[p].copy(), e[p].copy()
+    else:  # random windows: overlaps, gaps, inverted and empty ranges
+        b = rng.integers(0, n + 1, size=S).astype(np.uint32)
+        e = (b.astype(np.int64) + rng.integers(-5, 300, size=S)).clip(0, n).astype(np.uint32)
+    log(f"random segments seed={seed} n={n} S={S} {np.dtype(dt).name} kind={kind} layout={layout}")
+    d, db, de = g.to_dev(a), g.to_dev(b), g.to_dev(e)
+    out, idx = g.empty(S, dt), g.empty(S, np.uint32)
+    r = DeviceSegmentReduce()
+    for nm, op in (("Sum", o.OP_SUM), ("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        getattr(r, nm)(None, d, out, S, db, de)
+        assert (g.to_host(out) == o.segment_reduce(op, a, b, e)).all(), nm
+    for nm, is_max in (("ArgMin", False), ("ArgMax", True)):
+        getattr(r, nm)(None, d, out, idx, S, db, de)
+        ev, ei = o.segment_reduce_arg(is_max, a, b, e)
+        assert (g.to_host(out) == ev).all() and (g.to_host(idx) == ei).all(), nm
