@@ -394,7 +394,7 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
                 // wave's lowest-addressed segment sat in its second 64-element
                 // window).  The opaque copy keeps the whole offset in the VGPR.
                 uint32_t off = (cb + (uint32_t)j * kWave + lane + dl) * (uint32_t)sizeof(T);
-                asm volatile("" : "+v"(off));
+                asm("" : "+v"(off));
                 g[j] = buf_ld_elem_nt<T>(r, off);
             }
         } else {
@@ -559,8 +559,13 @@ __device__ __forceinline__ void wave_segments(const T *__restrict__ in, T *__res
     }
 }
 
+// Six waves per SIMD: the register allocator is held to 80 VGPRs (the gather
+// path's full-offset loads otherwise take Arg* of 4-byte types to 82, five
+// waves); nothing spills.  Interleaved A/B at C5 against the split-offset
+// loads, us: Sum 91.1 / 90.9, ArgMin 101.2 / 99.9; segments in a random
+// order, Sum 120.8 / 121.4, ArgMin 133.5 / 134.3.
 template <class T, int OP, bool FIXED>
-__global__ __launch_bounds__(kSegBlock) void segment_reduce_kernel(const T *__restrict__ in, T *__restrict__ out,
+__global__ __launch_bounds__(kSegBlock) __attribute__((amdgpu_waves_per_eu(6))) void segment_reduce_kernel(const T *__restrict__ in, T *__restrict__ out,
                                                                    uint32_t *__restrict__ index_out, uint64_t S,
                                                                    SegBounds sb, T init, int vec_ok)
 {
