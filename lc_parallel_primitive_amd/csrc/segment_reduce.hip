@@ -389,10 +389,11 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
                 // its lane part (lane + dl) is not: left to itself the compiler
                 // moves j * 64 (and cb) into the load's immediate / SGPR offset
                 // and passes the lane part as the VGPR offset, wrapped below
-                // zero.  The hardware does not add those two modulo 2^32: such
-                // loads returned wrong data (a random-order layout where a
-                // wave's lowest-addressed segment sat in its second 64-element
-                // window).  The opaque copy keeps the whole offset in the VGPR.
+                // zero.  Such loads are not reliably taken modulo 2^32: in a
+                // random-order layout (wave's lowest-addressed segment in its
+                // second 64-element window) a few of ~10^5 per launch read
+                // wrong data, different ones from launch to launch.  The
+                // opaque copy keeps the whole offset in the VGPR.
                 uint32_t off = (cb + (uint32_t)j * kWave + lane + dl) * (uint32_t)sizeof(T);
                 asm("" : "+v"(off));
                 g[j] = buf_ld_elem_nt<T>(r, off);
