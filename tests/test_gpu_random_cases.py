@@ -14,6 +14,9 @@ from oracle import oracle as o
 pytestmark = pytest.mark.gpu
 
 INT_DTYPES = [np.int32, np.uint32, np.int64, np.uint64]
+# Sizes are log-uniform in [2^LOG2_RANGE[0], 2^LOG2_RANGE[1]); the long-run
+# driver (tests/random_sweep.py) widens the range.
+LOG2_RANGE = (0, 20)
 
 
 def values(rng, dt, n, kind):
@@ -33,7 +36,7 @@ def values(rng, dt, n, kind):
 
 def case_params(seed):
     rng = np.random.default_rng(seed)
-    n = int(np.exp(rng.uniform(0, np.log(1 << 20))))
+    n = int(np.exp(rng.uniform(LOG2_RANGE[0] * np.log(2), LOG2_RANGE[1] * np.log(2))))
     return rng, n, INT_DTYPES[rng.integers(0, 4)], int(rng.integers(0, 4))
 
 
@@ -211,3 +214,77 @@ def test_random_misaligned_and_variants(gpu, seed):
     DeviceSegmentReduce().ArgMin(None, d, sout, sidx, S, size)
     ev, ei = o.segment_reduce_arg(False, a, b, e)
     assert (g.to_host(sout) == ev).all() and (g.to_host(sidx) == ei).all()
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_floats(gpu, seed):
+    """float32 / float64 data (normal at a random scale, few distinct values,
+    +-0, +-inf): sorts and Min/Max/Arg* exact against the oracle, sums and
+    scans within 1e-5 * sum|x| of float64 (finite data)."""
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce, DeviceScan, DeviceRadixSort, DeviceSegmentReduce
+
+    rng, n, _, kind = case_params(6000 + seed)
+    dt = [np.float32, np.float64][seed % 2]
+    if kind == 0:
+        a = rng.standard_normal(n) * 10 ** rng.uniform(-3, 3)
+    elif kind == 1:
+        a = rng.integers(-3, 4, size=n).astype(np.float64) * 0.5
+    elif kind == 2:
+        a = rng.standard_normal(n)
+        a[rng.random(n) < 0.05] = 0.0
+        a[rng.random(n) < 0.05] = -0.0
+    else:
+        a = rng.standard_normal(n)
+        a[rng.random(n) < 0.01] = np.inf
+        a[rng.random(n) < 0.01] = -np.inf
+    a = a.astype(dt)
+    finite = kind != 3
+    rt = 1e-5
+    log(f"random floats seed={seed} n={n} {np.dtype(dt).name} kind={kind}")
+    d = g.to_dev(a)
+    out, idx = g.empty(1, dt), g.empty(1, np.uint32)
+    r = DeviceReduce()
+    tmp = g.temp(DeviceReduce.GetTempStorageBytes(np.dtype(dt).name, n))
+    for nm, op in (("Min", o.OP_MIN), ("Max", o.OP_MAX)):
+        getattr(r, nm)(tmp, d, out, n)
+        assert g.to_host(out)[0] == o.reduce(op, a), nm
+    if finite:
+        r.Sum(tmp, d, out, n)
+        s, ab = o.reduce_f64(a)
+        assert abs(float(g.to_host(out)[0]) - s) <= rt * ab + 1e-30
+    tmpa = g.temp(DeviceReduce.GetArgTempStorageBytes(np.dtype(dt).name, n))
+    r.ArgMin(tmpa, d, out, idx, n)
+    v, i = o.reduce_arg(False, a)
+    assert g.to_host(out)[0] == v and g.to_host(idx)[0] == i
+    if finite:
+        so = g.empty(n, dt)
+        tmps = g.temp(DeviceScan.GetTempStorageBytes(np.dtype(dt).name, n))
+        DeviceScan().InclusiveSum(tmps, d, so, n)
+        ref, ab = o.scan_f64(a, True)
+        assert (np.abs(g.to_host(so).astype(np.float64) - ref) <= rt * ab + 1e-30).all()
+    desc = bool(rng.integers(0, 2))
+    ko, vo = g.empty(n, dt), g.empty(n, np.uint32)
+    v = np.arange(n, dtype=np.uint32)
+    tmp = g.temp(DeviceRadixSort.GetSortPairsTempStorageBytes(np.dtype(dt).name, "uint32", n))
+    srt = DeviceRadixSort()
+    (srt.SortPairsDescending if desc else srt.SortPairs)(tmp, d, ko, g.to_dev(v), vo, n)
+    rk, rv = o.radix_sort(a, v, descending=desc)
+    assert g.to_host(ko).tobytes() == rk.tobytes() and (g.to_host(vo) == rv).all()
+    S = max(1, int(rng.integers(1, 1 + max(1, n // int(rng.integers(1, 200))))))
+    cuts = np.sort(rng.integers(0, n + 1, size=S - 1))
+    bnd = np.concatenate([[0], cuts, [n]]).astype(np.uint32)
+    p = rng.permutation(S)
+    b, e = bnd[:-1][p].copy(), bnd[1:][p].copy()
+    db, de = g.to_dev(b), g.to_dev(e)
+    sout, sidx = g.empty(S, dt), g.empty(S, np.uint32)
+    seg = DeviceSegmentReduce()
+    seg.Max(None, d, sout, S, db, de)
+    assert (g.to_host(sout) == o.segment_reduce(o.OP_MAX, a, b, e)).all()
+    seg.ArgMax(None, d, sout, sidx, S, db, de)
+    ev, ei = o.segment_reduce_arg(True, a, b, e)
+    assert (g.to_host(sout) == ev).all() and (g.to_host(sidx) == ei).all()
+    if finite:
+        seg.Sum(None, d, sout, S, db, de)
+        s, ab = o.segment_reduce_f64(a, b, e)
+        assert (np.abs(g.to_host(sout).astype(np.float64) - s) <= rt * ab + 1e-30).all()
