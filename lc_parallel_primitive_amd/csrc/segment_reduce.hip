@@ -25,8 +25,9 @@
 //    concatenated into one virtual range and the same fold runs over it;
 //    each chunk is gathered with one load per element, 64 consecutive
 //    virtual elements per wave load, each element's segment found from a
-//    bitmap of the segment ends in the chunk.  A wave whose segments lie
-//    more than 4 GiB apart folds one segment at a time instead.
+//    bitmap of the segment ends in the chunk.  A wave whose segments span
+//    2 GiB or more (one buffer resource covers less) folds one segment at a
+//    time instead.
 //  * Segments longer than kSegLong: their indices are compacted into LDS and
 //    the whole workgroup streams each one (4 loads in flight per thread)
 //    after its waves are done.  Fixed-size segments longer than kSegLong
@@ -536,7 +537,7 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
     }
 }
 
-// A wave whose segments lie more than 4 GiB apart: one segment at a time,
+// A wave whose segments span 2 GiB or more: one segment at a time,
 // lane l folding elements l, l + 64, ... (long segments are left to the
 // workgroup path).
 template <class T, int OP>
@@ -597,12 +598,13 @@ __global__ __launch_bounds__(kSegBlock) __attribute__((amdgpu_waves_per_eu(6))) 
                                     s_flat.stage[wave], s_flat.gbits[wave], s_flat.gdelta[wave]);
     } else if (nvalid > 0) {
         const uint32_t vlen = is_long ? 0u : len;
-        // elements the gather reads: [lo, hi), at most 4 GiB for one buffer resource
+        // elements the gather reads: [lo, hi), under 2 GiB for one buffer
+        // resource (offsets stay below 2^31)
         uint32_t lo = wave_allreduce(vlen ? b : ~0u, MinOp());
         const uint32_t hi = wave_allreduce(vlen ? b + vlen : 0u, MaxOp());
         if (hi <= lo) lo = 0;  // nothing to read
         const uint64_t bytes = hi > lo ? (uint64_t)(hi - lo) * sizeof(T) : 0;
-        if (bytes <= 0xFFFFFFFFull) {
+        if (bytes <= 0x7FFFFFFFull) {
             const uint32_t vb = wave_inclusive_scan(vlen, SumOp()) - vlen;  // <= 64 * kSegLong
             flat_segments<T, OP, true>(in, out, index_out, init, wseg0, nvalid, vb, vlen, !is_long, b - lo - vb, lo,
                                        (uint32_t)bytes, s_flat.bnd[wave], s_flat.seg_of[wave], s_flat.bbits[wave],

@@ -464,6 +464,37 @@ def test_segments_more_than_4gib_apart(gpu):
     assert (i[empty] == 1).all()
 
 
+def test_segments_spanning_2_to_4_gib(gpu):
+    """Waves whose segments span 2-4 GiB of input (an int32 input of 3 * 2^28
+    elements, value = index): more than one buffer resource covers (offsets
+    would pass 2^31), so they fold one segment at a time; the
+    lowest-addressed segment of each wave comes last in it.  Results from
+    closed forms."""
+    import torch
+
+    n = 3 << 28
+    log("segment int32 3*2^28 gather spans 2-4 GiB")
+    d = torch.arange(n, dtype=torch.int32, device="cuda")
+    S = 256
+    rng = np.random.default_rng(12)
+    L = rng.integers(0, 200, S)
+    L[9] = 0
+    i = np.arange(S)
+    # even lanes near the end of the input, odd lanes near its start in
+    # descending order (the wave's lowest begin is its last odd lane)
+    b = np.where(i % 2 == 0, n - 40_000 + i * 100, (S - i) * 300).astype(np.int64)
+    e = np.minimum(b + L, n)
+    bu, eu = b.astype(np.uint32), e.astype(np.uint32)
+    sums = [(int((x + y - 1) * (y - x) // 2)) if y > x else 0 for x, y in zip(b, e)]
+    expect_sum = np.array([(v + 2**31) % 2**32 - 2**31 for v in sums], dtype=np.int64).astype(np.int32)
+    assert (seg_call("Sum", d, S, (bu, eu), np.int32) == expect_sum).all()
+    empty = e <= b
+    mx = seg_call("Max", d, S, (bu, eu), np.int32)
+    assert (mx[~empty] == e[~empty] - 1).all() and (mx[empty] == np.iinfo(np.int32).min).all()
+    v, ix = seg_call("ArgMin", d, S, (bu, eu), np.int32, arg=True)
+    assert (v[~empty] == b[~empty]).all() and (ix[~empty] == 0).all() and (ix[empty] == 1).all()
+
+
 def test_segments_at_the_top_of_the_32_bit_range(gpu):
     """Segments ending at element 2^32 - 1 (an int32 input of 2^32 - 1
     elements, 16 GiB): a tiling layout there is past the contiguous path's
