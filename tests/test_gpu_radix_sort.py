@@ -420,3 +420,31 @@ def test_pairs_stable_above_2p30(gpu):
     del v
     assert datagen.check_stable_pairs_u32(k, ko, vo) == 0
     del k, ko, vo
+
+
+def test_keys_at_the_32_bit_limit(gpu):
+    """n = 2^32 - 1 uint32 keys, the largest sort that 32-bit positions and
+    counts allow (262 144 tiles, the last one a single key short): sorted, the
+    same multiset as the input, and a guard region past the output (where
+    the last tile's pad would land) untouched."""
+    import torch
+
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceRadixSort, datagen
+
+    n = (1 << 32) - 1
+    guard = 0x5A5A5A5A
+    log(f"sort keys u32 n={n}")
+    d = datagen.keys_u32(n, seed=0x2B32)
+    h_in = datagen.sorted_hash_u32(d)
+    buf = torch.full((n + 256,), guard, dtype=torch.int32, device="cuda")
+    out = buf.view(torch.uint32)[:n]
+    tmp = g.temp(DeviceRadixSort.GetSortKeysTempStorageBytes("uint32", n))
+    DeviceRadixSort().SortKeys(tmp, d, out, n)
+    torch.cuda.synchronize()
+    del d, tmp
+    h_out = datagen.sorted_hash_u32(out)
+    assert h_out[0] == 0 and h_out[1:] == h_in[1:]
+    assert bool((buf[n:] == guard).all())
+    del buf, out
+    torch.cuda.empty_cache()
