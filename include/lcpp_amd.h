@@ -224,7 +224,7 @@ int lcpp_reduce_by_key(lcpp_dtype k, lcpp_dtype v, lcpp_reduce_op op, void *temp
  * DeviceRadixSort (onesweep, all key bits) — device/device_radix_sort.h
  * Keys: any lcpp_dtype (signed and floating keys are bit-twiddled as in
  * common/util_type.h:98-175; -0.0 and +0.0 compare equal).  Values: any
- * lcpp_dtype (moved as raw 4- or 8-byte words).  n < 2^30.
+ * lcpp_dtype (moved as raw 4- or 8-byte words).  n < 2^32.
  * ------------------------------------------------------------------- */
 /* replaces DeviceRadixSort::GetSortKeysTempStorageBytes<K>(num_items), device_radix_sort.h:118-122 */
 int lcpp_radix_sort_keys_temp_bytes(lcpp_dtype k, uint64_t n, size_t *bytes);
