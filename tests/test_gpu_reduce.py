@@ -225,3 +225,22 @@ def test_transform_vs_oracle(gpu, dtype, op, xf):
         assert abs(float(got) - s) <= RTOL_SUM * ab
     else:
         assert got == o.reduce_transform(OPS[op], XFS[xf], a, init)
+
+
+def test_past_2p32_elements(gpu):
+    """Sum of n = 2^32 + 12345 int32 ones wraps to 12345; ArgMax/ArgMin over
+    n = 2^32 - 1 elements (the most that 32-bit indices allow): ties of ones
+    go to the last / first index, and a lone 0 at the last index is found."""
+    import torch
+
+    n = (1 << 32) + 12345
+    log(f"reduce int32 ones n={n}")
+    d = torch.ones(n, dtype=torch.int32, device="cuda")
+    assert int(run("Sum", d, n, np.int32)) == 12345
+    m = (1 << 32) - 1
+    assert run_arg(True, d, m, np.int32) == (1, m - 1)
+    assert run_arg(False, d, m, np.int32) == (1, 0)
+    d[m - 1] = 0
+    assert run_arg(False, d, m, np.int32) == (0, m - 1)
+    del d
+    torch.cuda.empty_cache()

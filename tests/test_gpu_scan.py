@@ -126,3 +126,32 @@ def test_ragged_tile_writes_nothing_past_the_end(gpu, dtype, n, pad):
         h = g.to_host(out)
         assert (h[:n] == o.scan(a, incl)).all()
         assert (h[n:] == 77).all(), "store past the end of the output"
+
+
+@pytest.mark.parametrize("kind", ["ExclusiveSum", "InclusiveSum"])
+def test_past_2p32_elements_ones(gpu, kind):
+    """n = 2^32 + 12345 uint32 ones (16 GiB; element offsets and positions
+    past 32 bits): the scan of ones is the index (exclusive) or the index
+    plus one (inclusive) mod 2^32, compared on the device against the
+    generator's 32-bit index."""
+    import torch
+
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceScan, datagen
+
+    n = (1 << 32) + 12345
+    log(f"scan u32 {kind} ones n={n}")
+    d = torch.ones(n, dtype=torch.int32, device="cuda").view(torch.uint32)
+    out = torch.empty(n, dtype=torch.uint32, device="cuda")
+    tmp = g.temp(DeviceScan.GetTempStorageBytes("uint32", n))
+    getattr(DeviceScan(), kind)(tmp, d, out, n)
+    del d, tmp
+    idx = datagen.iota_u32(n)
+    o = out.view(torch.int32)
+    if kind == "ExclusiveSum":
+        ok = bool((o == idx.view(torch.int32)).all())
+    else:
+        ok = bool((o[:-1] == idx.view(torch.int32)[1:]).all()) and int(o[-1]) == (n & 0xFFFFFFFF)
+    del out, idx, o
+    torch.cuda.empty_cache()
+    assert ok
