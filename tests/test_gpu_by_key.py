@@ -298,3 +298,39 @@ def test_full_size_2p28(gpu):
     r = int(g.to_host(runs)[0])
     assert r == ek.size
     assert (g.to_host(uk)[:r] == ek).all() and (g.to_host(ag)[:r] == ea).all()
+
+
+def test_at_the_32_bit_limit(gpu):
+    """n = 2^32 - 1 int32 keys in runs of 128 (key = index >> 7 of the 32-bit
+    index; the last run holds 127) and int32 ones: ReduceByKey finds 2^25
+    runs, each summing to its length, with the runs' keys; InclusiveSumByKey
+    gives the position within the run plus one."""
+    import torch
+
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce, DeviceScan, datagen
+
+    n = (1 << 32) - 1
+    log(f"ReduceByKey / InclusiveSumByKey int32 n={n}")
+    dk = datagen.iota_u32(n).view(torch.int32)
+    dk >>= 7
+    dv = torch.ones(n, dtype=torch.int32, device="cuda")
+    uk = torch.empty(n, dtype=torch.int32, device="cuda")
+    ag = torch.empty(n, dtype=torch.int32, device="cuda")
+    runs = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tmp = g.temp(DeviceReduce.GetReduceByKeyTempStorageBytes("int32", "int32", n))
+    DeviceReduce().ReduceByKey(tmp, dk, dv, uk, ag, runs, "sum", n)
+    r = int(runs.cpu()[0])
+    assert r == 1 << 25
+    assert bool((uk[:r] == dk[::128]).all())
+    assert bool((ag[: r - 1] == 128).all()) and int(ag[r - 1]) == 127
+    del uk, ag, tmp
+    out = torch.empty(n, dtype=torch.int32, device="cuda")
+    tmp = g.temp(DeviceScan.GetScanByKeyTempStorageBytes("int32", "int32", n))
+    DeviceScan().InclusiveSumByKey(tmp, dk, dv, out, n)
+    step = torch.arange(1, 129, dtype=torch.int32, device="cuda")
+    full = n - 127
+    assert bool((out[:full].view(-1, 128) == step).all())
+    assert bool((out[full:] == step[:127]).all())
+    del dk, dv, out, tmp
+    torch.cuda.empty_cache()
