@@ -290,6 +290,24 @@ __device__ __forceinline__ void flat_seg_scan(bool &f, typename Acc::A &v)
     step(dpp_move<kDppRowBcast31, 0xC>((int)f, 0), Acc::template dpp_mv<kDppRowBcast31, 0xC>(v, id));
 }
 
+// The element range [B, E) a wave's flat pass reads: the first begin and the
+// last end of its NON-EMPTY segments (lanes < nvalid, in lane order; B = E = 0
+// when every segment is empty).  An empty segment (end <= begin) need not lie
+// inside the input at all, so it never widens the range: taking E from a
+// last lane that is an empty segment with its begin past the input would let
+// the wave's loads run past the input allocation.  Wave-uniform.
+__device__ __forceinline__ void flat_range(uint32_t nvalid, uint32_t b, uint32_t len, uint32_t &B, uint32_t &E)
+{
+    const uint64_t ne = ballot(lane_id() < nvalid && len > 0);
+    if (ne == 0) {
+        B = E = 0;
+        return;
+    }
+    const int first = __builtin_ctzll(ne), last = 63 - __builtin_clzll(ne);
+    B = (uint32_t)__builtin_amdgcn_readlane((int)b, first);
+    E = (uint32_t)__builtin_amdgcn_readlane((int)(b + len), last);
+}
+
 // Whether the wave's segments take the flat path: sorted, not overlapping,
 // none long, gaps holding at most as many elements as the segments plus one
 // chunk, and a range end below kFlatMaxEnd.  Wave-uniform.
@@ -301,8 +319,8 @@ __device__ __forceinline__ bool flat_eligible(uint32_t nvalid, uint32_t b, uint3
     const uint32_t b_next = (uint32_t)__shfl_down((int)b, 1);
     const bool breaks = lane < nvalid && (len > kSegLong || (lane + 1 < nvalid && b + len > b_next));
     if (nvalid == 0 || ballot(breaks) != 0) return false;
-    const uint32_t B = (uint32_t)__builtin_amdgcn_readfirstlane((int)b);
-    const uint32_t E = (uint32_t)__builtin_amdgcn_readlane((int)(b + len), (int)nvalid - 1);
+    uint32_t B, E;
+    flat_range(nvalid, b, len, B, E);
     const uint32_t total = wave_allreduce(lane < nvalid ? len : 0u, SumOp());  // <= 64 * kSegLong
     return E <= kFlatMaxEnd && (uint64_t)(E - B) <= 2ull * total + CH;
 }
@@ -336,8 +354,8 @@ __device__ __forceinline__ void flat_segments(const T *__restrict__ in, T *__res
     const uint32_t lane = lane_id();
     const bool valid = lane < nvalid;
     const uint32_t e = b + len;
-    const uint32_t B = (uint32_t)__builtin_amdgcn_readfirstlane((int)b);
-    const uint32_t E = (uint32_t)__builtin_amdgcn_readlane((int)e, (int)nvalid - 1);
+    uint32_t B, E;
+    flat_range(nvalid, b, len, B, E);
     // segments in order of their ends: the non-empty ones get ranks (their
     // ends are distinct and increasing), seg_of maps a rank to its segment
     const bool nonempty = valid && len > 0;

@@ -62,6 +62,45 @@ def test_arbitrary_ranges_long_empty_inverted(gpu):
     assert (run(g.to_dev(a), b, e, np.int32) == o.segment_reduce(o.OP_SUM, a, b, e)).all()
 
 
+def test_flat_wave_ending_in_empty_segments_past_the_input(gpu):
+    """A wave whose sorted segments tile the end of the input and whose last
+    lanes are empty or inverted segments with begins past the input.  Only
+    end <= begin makes a segment empty, so its begin may lie anywhere: the
+    flat path must take its read window from the non-empty segments.  The
+    input is a whole 16 MiB allocation (torch gives sizes of 10 MiB and more
+    a segment of their own, rounded to 2 MiB), so a read past n would leave
+    the mapping; n * 4 is a multiple of 16, so no 16-byte load straddles n."""
+    import gpu_util as g
+    import torch
+
+    n = 4 << 20
+    rng = np.random.default_rng(2024)
+    T = 64 * 512 + 20  # the last wave: 20 tiling segments, then 44 empty ones
+    cuts = np.sort(rng.choice(np.arange(1, n), T - 1, replace=False)).astype(np.int64)
+    b = np.concatenate([[0], cuts]).astype(np.uint32)
+    e = np.concatenate([cuts, [n]]).astype(np.uint32)
+    eb = (n + 7 * np.arange(44)).astype(np.uint32)
+    ee = eb.copy()
+    ee[1::2] = eb[1::2] // 2  # inverted: end < begin
+    b, e = np.concatenate([b, eb]), np.concatenate([e, ee])
+    S = b.size
+    log(f"segment flat wave ending past the input n={n} S={S}")
+    for dtype in (np.int32, np.float32):
+        a = g.random_array(dtype, n, seed=11)
+        d = torch.empty(n, dtype=g._NP2T[np.dtype(dtype)], device="cuda")  # exactly 16 MiB
+        d.copy_(torch.from_numpy(a))
+        got = seg_call("Sum", d, S, (b, e), dtype)
+        if dtype == np.int32:
+            assert same(got, o.segment_reduce(o.OP_SUM, a, b, e))
+        else:
+            s, ab = o.segment_reduce_f64(a, b, e)
+            assert (np.abs(got.astype(np.float64) - s) <= RTOL_SEG * ab + 1e-30).all()
+        assert same(seg_call("Max", d, S, (b, e), dtype), o.segment_reduce(o.OP_MAX, a, b, e))
+        v, i = seg_call("ArgMin", d, S, (b, e), dtype, arg=True)
+        ev, ei = o.segment_reduce_arg(False, a, b, e)
+        assert same(v, ev) and (i == ei).all()
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_floats_vs_float64(gpu, dtype):
     import gpu_util as g
