@@ -356,7 +356,21 @@ def main():
                                                  ctypes.c_void_p(uk.data_ptr()), ctypes.c_void_p(ag.data_ptr()),
                                                  ctypes.c_void_p(nr.data_ptr()), n, sp), "rbk"),
                 20, "reduce_by_key_tile")
-            del k, x, uk, ag, t1
+            # the first 3/4 in runs of mean 128 (tiles that stage their runs and
+            # publish only PARTIAL run counts), then all-distinct keys (dense
+            # tiles, whose run-count look-back walks back over the staged stretch)
+            q = 3 * n // 4
+            k2 = k.clone()
+            k2[q:] = k2[q - 1] + 1 + torch.arange(n - q, dtype=torch.int32, device="cuda")
+            runs2 = int(k2[q - 1].item()) - int(k2[0].item()) + 1 + (n - q)
+            add("DeviceReduce::ReduceByKey sum int32 keys (3/4 runs of mean 128, then all distinct) -> float32 "
+                "N=2^28", 8 * n + 8 * runs2,
+                lambda: chk(L.lcpp_reduce_by_key(I32, F32, 0, ctypes.c_void_p(t1.data_ptr()), tb,
+                                                 ctypes.c_void_p(k2.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                                 ctypes.c_void_p(uk.data_ptr()), ctypes.c_void_p(ag.data_ptr()),
+                                                 ctypes.c_void_p(nr.data_ptr()), n, sp), "rbk"),
+                20, "reduce_by_key_tile")
+            del k, k2, x, uk, ag, t1
         if want("segment"):
             n, S = 1 << 27, 1 << 20
             x = datagen.normal_f32(n, seed=datagen.SEED_SEG_VALUES)

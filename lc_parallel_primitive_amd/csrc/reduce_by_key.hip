@@ -220,7 +220,9 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
         if (wave == 0) {
             uint32_t p = 0;
             if (tile > 0) {
-                p = lb_wait_prefix(tcwords, tile, SumOp(), 0u, ctl);
+                // staged tiles publish only PARTIAL counts: a tile after a
+                // long staged stretch walks it 512 words per round trip
+                p = lb_wait_prefix_wide<8>(tcwords, tile, SumOp(), 0u, ctl);
                 if (lane == 0) lb_publish(tcwords, tile, p + sm.tc, kStInclusive, ctl);
             }
             if (lane == 0) s_cpre = p;

@@ -259,6 +259,29 @@ def test_reduce_by_key_dense_and_sparse_tiles_mixed(gpu, op):
     assert (uk[r:] == 0).all() and (ag[r:] == 0).all()
 
 
+@pytest.mark.parametrize("n_staged_tiles", [15, 16, 17, 600, 3000])
+def test_reduce_by_key_long_staged_prefix_then_dense(gpu, n_staged_tiles):
+    """A long stretch of tiles that stage their runs (they publish only
+    PARTIAL counts) followed by dense tiles, whose run-count look-back walks
+    the whole stretch: 15/16/17 tiles end the walk inside or just past its
+    first 16-word round trip; 600 and 3000 take several 512-word trips."""
+    tile = 8192
+    n = (n_staged_tiles + 6) * tile + 333
+    rng = np.random.default_rng(n_staged_tiles)
+    mean = np.full(n, 700.0)
+    mean[n_staged_tiles * tile:] = 1.5  # dense from here on
+    heads = rng.random(n) < 1.0 / mean
+    heads[0] = True
+    keys = np.cumsum(heads, dtype=np.int64).astype(np.uint32)
+    v = values(np.uint32, n, 3)
+    log(f"ReduceByKey {n_staged_tiles} staged tiles, then dense")
+    uk, ag, r = reduce_by_key(keys, v, "sum", guard=8)
+    ek, ea = o.reduce_by_key(keys, v)
+    assert r == ek.size
+    assert (uk[:r] == ek).all() and (ag[:r] == ea).all()
+    assert (uk[r:] == 0).all() and (ag[r:] == 0).all()
+
+
 def test_reduce_by_key_empty_and_single(gpu):
     uk, ag, r = reduce_by_key(np.empty(0, np.int32), np.empty(0, np.int32))
     assert r == 0
