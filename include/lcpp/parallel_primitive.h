@@ -254,6 +254,27 @@ class DeviceScan : public LuisaModule {
         lcpp_scan_temp_bytes(dtype_of<T>(), num_items, &b);
         return b;
     }
+    /* device/device_scan.h:114-145 (scan_op: SumOp, MinOp or MaxOp):
+     * d_out[i] = scan_op(initial_value, d_in[0..i)) */
+    template <class T, class ScanOp>
+    void ExclusiveScan(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                       size_t num_items, ScanOp, T initial_value)
+    {
+        check(lcpp_scan_exclusive(dtype_of<T>(), reduce_op_of<ScanOp>(), temp_storage.data(),
+                                  temp_storage.size_bytes(), d_in.data(), d_out.data(), num_items, &initial_value,
+                                  cmdlist.stream),
+              "DeviceScan::ExclusiveScan", cmdlist.stream, temp_storage);
+    }
+    /* device/device_scan.h:147-178: d_out[i] = scan_op(initial_value, d_in[0..i]) */
+    template <class T, class ScanOp>
+    void InclusiveScan(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                       size_t num_items, ScanOp, T initial_value)
+    {
+        check(lcpp_scan_inclusive(dtype_of<T>(), reduce_op_of<ScanOp>(), temp_storage.data(),
+                                  temp_storage.size_bytes(), d_in.data(), d_out.data(), num_items, &initial_value,
+                                  cmdlist.stream),
+              "DeviceScan::InclusiveScan", cmdlist.stream, temp_storage);
+    }
     template <class T>
     void ExclusiveSum(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
                       size_t num_items)

@@ -166,6 +166,18 @@ int lcpp_scan_exclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const v
 /* replaces DeviceScan::InclusiveSum, device_scan.h:193-204: out[i] = sum(in[0..i]) */
 int lcpp_scan_inclusive_sum(lcpp_dtype t, void *temp, size_t temp_bytes, const void *in,
                             void *out, uint64_t n, void *stream);
+/* replaces DeviceScan::ExclusiveScan(cmdlist, temp, d_in, d_out, num_items, scan_op,
+ * initial_value), device_scan.h:114-145: out[i] = op(init, in[0..i)), so out[0] = init.
+ * *init is a host value of type t (NULL: the op's identity, 0 for the sum).  Temp storage as
+ * for lcpp_scan_temp_bytes.  (The reference folds initial_value in once per warp in its first
+ * tile, block/detail/block_scan_warp.h:223-236; with an init other than the op's identity
+ * its sums differ from this definition, which follows CUB's.) */
+int lcpp_scan_exclusive(lcpp_dtype t, lcpp_reduce_op op, void *temp, size_t temp_bytes, const void *in,
+                        void *out, uint64_t n, const void *init, void *stream);
+/* replaces DeviceScan::InclusiveScan(cmdlist, temp, d_in, d_out, num_items, scan_op,
+ * initial_value), device_scan.h:147-178: out[i] = op(init, in[0..i]). */
+int lcpp_scan_inclusive(lcpp_dtype t, lcpp_reduce_op op, void *temp, size_t temp_bytes, const void *in,
+                        void *out, uint64_t n, const void *init, void *stream);
 /* No counterpart in the reference.  For callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the
  * same result as lcpp_scan_exclusive_sum with no temp argument and no allocation.

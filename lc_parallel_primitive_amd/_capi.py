@@ -39,6 +39,8 @@ SIGNATURES = {
     "lcpp_scan_temp_bytes": (_i, [_i, _u64, _c_size_p]),
     "lcpp_scan_exclusive_sum": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
     "lcpp_scan_inclusive_sum": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
+    "lcpp_scan_exclusive": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp, _vp]),
+    "lcpp_scan_inclusive": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp, _vp]),
     "lcpp_scan_exclusive_sum_noalloc": (_i, [_i, _vp, _vp, _u64, _vp]),
     "lcpp_radix_sort_keys_temp_bytes": (_i, [_i, _u64, _c_size_p]),
     "lcpp_radix_sort_keys": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),

@@ -1,4 +1,5 @@
-// scan.hip — DeviceScan::ExclusiveSum/InclusiveSum for gfx950.
+// scan.hip — DeviceScan::ExclusiveScan/InclusiveScan (Sum, Min, Max with an
+// initial value) and ExclusiveSum/InclusiveSum for gfx950.
 //
 // Reference: device/device_scan.h:114-204, 349-411 (init kernel + one
 // single-pass scan kernel), device/details/scan.h:59-147,
@@ -30,6 +31,8 @@
 //    (release/acquire pairs cost an L2 write-back/invalidate per publish on
 //    this part: 7.8 ms for 2^27 x 64-bit); wave 0 polls 16 predecessors at
 //    once and stops at the nearest INCLUSIVE.
+#include <cstring>
+
 #include "lookback.hpp"
 
 namespace lcpp {
@@ -79,11 +82,13 @@ constexpr int scan_min_waves()
 {
     return sizeof(T) == 4 && !(INCLUSIVE && std::is_same<T, float>::value) ? 4 : 1;
 }
-template <class T, bool INCLUSIVE>
+// out[i] = op(init, in[0..i)) (exclusive) or op(init, in[0..i]) (inclusive);
+// op is SumOp, MinOp or MaxOp (commutative: the look-back folds windows as
+// trees).  The Sum scans are init = 0.
+template <class T, bool INCLUSIVE, class Op>
 __global__ __launch_bounds__(kScanBlock) __attribute__((amdgpu_waves_per_eu(scan_min_waves<T, INCLUSIVE>())))
-void scan_kernel(const T *__restrict__ in,
-                                                          T *__restrict__ out, uint64_t n,
-                                                          uint64_t *words, int vec_ok, WaitCtl ctl)
+void scan_kernel(const T *__restrict__ in, T *__restrict__ out, uint64_t n, uint64_t *words, int vec_ok, T init,
+                 WaitCtl ctl)
 {
     constexpr int V = 16 / sizeof(T);
     constexpr int K = scan_vecs<T, INCLUSIVE>();
@@ -93,7 +98,8 @@ void scan_kernel(const T *__restrict__ in,
     __shared__ T s_wtot[K][W];
     __shared__ T s_prefix;
 
-    SumOp op;
+    Op op;
+    const T id = Op::template identity<T>();
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
@@ -126,7 +132,7 @@ void scan_kernel(const T *__restrict__ in,
             r = x[k][V - 1];
         } else {
             r = x[k][0];
-            x[k][0] = T(0);
+            x[k][0] = id;
 #pragma unroll
             for (int j = 1; j < V; ++j) {
                 const T v = x[k][j];
@@ -135,19 +141,19 @@ void scan_kernel(const T *__restrict__ in,
             }
         }
         const T inc = wave_inclusive_scan(r, op);
-        const T wex = wave_shr1(inc, T(0));
+        const T wex = wave_shr1(inc, id);
         if (lane == kWave - 1) s_wtot[k][wave] = inc;
 #pragma unroll
         for (int j = 0; j < V; ++j) x[k][j] = op(wex, x[k][j]);
     }
     __syncthreads();
     if (wave == 0) {
-        T agg = T(0);
+        T agg = id;
 #pragma unroll
         for (int k = 0; k < K; ++k)
 #pragma unroll
             for (int w = 0; w < W; ++w) agg = op(agg, s_wtot[k][w]);
-        const T ex = lb_scan_tile(words, tile, agg, op, T(0), ctl);
+        const T ex = lb_scan_tile_init(words, tile, agg, op, id, init, ctl);
         if (lane == 0) s_prefix = ex;
     }
     __syncthreads();
@@ -156,7 +162,7 @@ void scan_kernel(const T *__restrict__ in,
     T run = s_prefix;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        T pre = T(0), tot = T(0);
+        T pre = id, tot = id;
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             const T v = s_wtot[k][w];
@@ -182,8 +188,8 @@ void scan_kernel(const T *__restrict__ in,
 // Enqueue one scan whose status header + look-back words start at `head`
 // (zeroed here by a fill kernel, so the call can be graph-captured).
 // `instrument`: bracket the launches with the profiling events when enabled.
-template <class T>
-int scan_run(bool inclusive, uint64_t *head, const T *in, T *out, uint64_t n, uint64_t tiles, hipStream_t s,
+template <class T, class Op>
+int scan_run(bool inclusive, uint64_t *head, const T *in, T *out, uint64_t n, uint64_t tiles, T init, hipStream_t s,
              bool instrument)
 {
     uint64_t *words = head + kStatusBytes / 8;
@@ -194,26 +200,29 @@ int scan_run(bool inclusive, uint64_t *head, const T *in, T *out, uint64_t n, ui
         if (lb_init(head, nwords, s, "scan_init") != LCPP_OK) return LCPP_ERR_HIP;
         if (inclusive)
             LCPP_LAUNCH("scan_inclusive", s,
-                        scan_kernel<T, true><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
+                        (scan_kernel<T, true, Op><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok,
+                                                                                          init, ctl)));
         else
             LCPP_LAUNCH("scan_exclusive", s,
-                        scan_kernel<T, false><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl));
+                        (scan_kernel<T, false, Op><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok,
+                                                                                           init, ctl)));
     } else {
         const uint64_t g = ceil_div(nwords, 256);
         lb_init_kernel<<<(uint32_t)(g < 1024 ? g : 1024), 256, 0, s>>>(head, nwords);
         if (hipGetLastError() != hipSuccess) return LCPP_ERR_HIP;
         if (inclusive)
-            scan_kernel<T, true><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl);
+            scan_kernel<T, true, Op><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, init, ctl);
         else
-            scan_kernel<T, false><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, ctl);
+            scan_kernel<T, false, Op><<<(uint32_t)tiles, kScanBlock, 0, s>>>(in, out, n, words, vec_ok, init, ctl);
     }
     LCPP_CHECK_LAUNCH();
     return LCPP_OK;
 }
 
-template <class T>
-int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, void *out_,
-                uint64_t n, hipStream_t s)
+// `init_`: a host value of type T, or NULL for the operator's identity.
+template <class T, class Op>
+int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, void *out_, uint64_t n,
+                const void *init_, hipStream_t s)
 {
     if (n == 0) return LCPP_OK;
     const T *in = static_cast<const T *>(in_);
@@ -223,20 +232,34 @@ int scan_launch(bool inclusive, void *temp, size_t temp_bytes, const void *in_, 
     if (tiles > 0xFFFFFFFFull) return LCPP_ERR_INVALID_ARG;
     if (temp_bytes < scan_temp_bytes<T>(n)) return LCPP_ERR_TEMP_TOO_SMALL;
     if (!temp || (reinterpret_cast<uintptr_t>(temp) & 255)) return LCPP_ERR_INVALID_ARG;
-    return scan_run<T>(inclusive, static_cast<uint64_t *>(temp), in, out, n, tiles, s, true);
+    T init = Op::template identity<T>();
+    if (init_) memcpy(&init, init_, sizeof(T));
+    return scan_run<T, Op>(inclusive, static_cast<uint64_t *>(temp), in, out, n, tiles, init, s, true);
 }
 
-int scan_dispatch(bool inclusive, lcpp_dtype t, void *temp, size_t tb, const void *in, void *out,
-                  uint64_t n, void *stream)
+template <class T>
+int scan_op_dispatch(bool inclusive, lcpp_reduce_op op, void *temp, size_t tb, const void *in, void *out, uint64_t n,
+                     const void *init, hipStream_t s)
+{
+    switch (op) {
+    case LCPP_OP_SUM: return scan_launch<T, SumOp>(inclusive, temp, tb, in, out, n, init, s);
+    case LCPP_OP_MIN: return scan_launch<T, MinOp>(inclusive, temp, tb, in, out, n, init, s);
+    case LCPP_OP_MAX: return scan_launch<T, MaxOp>(inclusive, temp, tb, in, out, n, init, s);
+    default: return LCPP_ERR_INVALID_ARG;
+    }
+}
+
+int scan_dispatch(bool inclusive, lcpp_dtype t, lcpp_reduce_op op, void *temp, size_t tb, const void *in, void *out,
+                  uint64_t n, const void *init, void *stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (t) {
-    case LCPP_INT32: return scan_launch<int32_t>(inclusive, temp, tb, in, out, n, s);
-    case LCPP_UINT32: return scan_launch<uint32_t>(inclusive, temp, tb, in, out, n, s);
-    case LCPP_FLOAT32: return scan_launch<float>(inclusive, temp, tb, in, out, n, s);
-    case LCPP_INT64: return scan_launch<int64_t>(inclusive, temp, tb, in, out, n, s);
-    case LCPP_UINT64: return scan_launch<uint64_t>(inclusive, temp, tb, in, out, n, s);
-    case LCPP_FLOAT64: return scan_launch<double>(inclusive, temp, tb, in, out, n, s);
+    case LCPP_INT32: return scan_op_dispatch<int32_t>(inclusive, op, temp, tb, in, out, n, init, s);
+    case LCPP_UINT32: return scan_op_dispatch<uint32_t>(inclusive, op, temp, tb, in, out, n, init, s);
+    case LCPP_FLOAT32: return scan_op_dispatch<float>(inclusive, op, temp, tb, in, out, n, init, s);
+    case LCPP_INT64: return scan_op_dispatch<int64_t>(inclusive, op, temp, tb, in, out, n, init, s);
+    case LCPP_UINT64: return scan_op_dispatch<uint64_t>(inclusive, op, temp, tb, in, out, n, init, s);
+    case LCPP_FLOAT64: return scan_op_dispatch<double>(inclusive, op, temp, tb, in, out, n, init, s);
     default: return LCPP_ERR_UNSUPPORTED_DTYPE;
     }
 }
@@ -266,13 +289,25 @@ extern "C" int lcpp_scan_temp_bytes(lcpp_dtype t, uint64_t n, size_t *bytes)
 extern "C" int lcpp_scan_exclusive_sum(lcpp_dtype t, void *temp, size_t tb, const void *in,
                                        void *out, uint64_t n, void *stream)
 {
-    return scan_dispatch(false, t, temp, tb, in, out, n, stream);
+    return scan_dispatch(false, t, LCPP_OP_SUM, temp, tb, in, out, n, nullptr, stream);
 }
 
 extern "C" int lcpp_scan_inclusive_sum(lcpp_dtype t, void *temp, size_t tb, const void *in,
                                        void *out, uint64_t n, void *stream)
 {
-    return scan_dispatch(true, t, temp, tb, in, out, n, stream);
+    return scan_dispatch(true, t, LCPP_OP_SUM, temp, tb, in, out, n, nullptr, stream);
+}
+
+extern "C" int lcpp_scan_exclusive(lcpp_dtype t, lcpp_reduce_op op, void *temp, size_t tb, const void *in, void *out,
+                                   uint64_t n, const void *init, void *stream)
+{
+    return scan_dispatch(false, t, op, temp, tb, in, out, n, init, stream);
+}
+
+extern "C" int lcpp_scan_inclusive(lcpp_dtype t, lcpp_reduce_op op, void *temp, size_t tb, const void *in, void *out,
+                                   uint64_t n, const void *init, void *stream)
+{
+    return scan_dispatch(true, t, op, temp, tb, in, out, n, init, stream);
 }
 
 // ---------------------------------------------------------------- no-allocation variant
@@ -317,7 +352,7 @@ int scan_noalloc(const void *in_, void *out_, uint64_t n, hipStream_t s)
     if (kStatusBytes / 8 + tiles * (sizeof(T) == 4 ? 1 : 2) > kNoAllocWords) return LCPP_ERR_SIZE_LIMIT;
     uint64_t *head = nullptr;
     if (scratch_ptr(&head) != LCPP_OK) return LCPP_ERR_HIP;
-    return scan_run<T>(false, head, in, out, n, tiles, s, false);
+    return scan_run<T, SumOp>(false, head, in, out, n, tiles, T(0), s, false);
 }
 }  // namespace
 

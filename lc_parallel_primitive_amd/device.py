@@ -186,7 +186,8 @@ class DeviceReduce(_Module):
 
 
 class DeviceScan(_Module):
-    """device/device_scan.h:33-339 (ExclusiveSum / InclusiveSum / *ScanByKey / *SumByKey)."""
+    """device/device_scan.h:33-339 (ExclusiveScan / InclusiveScan / ExclusiveSum / InclusiveSum / *ScanByKey /
+    *SumByKey)."""
 
 
     @staticmethod
@@ -205,6 +206,28 @@ class DeviceScan(_Module):
 
     def InclusiveSum(self, temp_storage, d_in, d_out, num_items: int, stream=None):
         self._run(lib().lcpp_scan_inclusive_sum, temp_storage, d_in, d_out, num_items, stream)
+
+    def _scan_op(self, fn, name, temp, d_in, d_out, num_items, op, init, stream):
+        _need(d_in, num_items, "d_in")
+        _need(d_out, num_items, "d_out")
+        _same_dtype(d_in, d_out, name)
+        if op not in LCPP_OPS:
+            raise ValueError(f"{name}: unsupported scan_op {op!r}")
+        code = dtype_code(d_in.dtype)
+        iv = _host_value(code, init)
+        self._check(fn(code, LCPP_OPS[op], _ptr(temp), _nbytes(temp), _ptr(d_in), _ptr(d_out), num_items,
+                       ctypes.c_void_p(iv.ctypes.data), _stream(stream)), name, temp, stream)
+
+    def ExclusiveScan(self, temp_storage, d_in, d_out, num_items: int, scan_op: str, initial_value, stream=None):
+        """device_scan.h:114-145: out[i] = scan_op(initial_value, d_in[0..i)), out[0] = initial_value.
+        scan_op: "sum" | "min" | "max"."""
+        self._scan_op(lib().lcpp_scan_exclusive, "ExclusiveScan", temp_storage, d_in, d_out, num_items, scan_op,
+                      initial_value, stream)
+
+    def InclusiveScan(self, temp_storage, d_in, d_out, num_items: int, scan_op: str, initial_value, stream=None):
+        """device_scan.h:147-178: out[i] = scan_op(initial_value, d_in[0..i])."""
+        self._scan_op(lib().lcpp_scan_inclusive, "InclusiveScan", temp_storage, d_in, d_out, num_items, scan_op,
+                      initial_value, stream)
 
     @staticmethod
     def GetScanByKeyTempStorageBytes(key_dtype, value_dtype, num_items: int) -> int:

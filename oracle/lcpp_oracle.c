@@ -406,6 +406,30 @@ int lcor_scan(int inclusive, int dtype, const void *in, void *out, uint64_t n)
     return 0;
 }
 
+/* DeviceScan::ExclusiveScan / InclusiveScan (device/device_scan.h:114-178)
+ * with scan_op Sum/Min/Max and initial_value, as CUB defines them: a left
+ * fold that starts from init, out_i = op(init, x_0, ..., x_{i-1}) (exclusive)
+ * or op(init, x_0, ..., x_i) (inclusive).  Integer sums wrap; Min/Max use the
+ * comparisons of fold_any.  init NULL = the op's identity.  (The reference's
+ * first tile folds initial_value in once per warp, block_scan_warp.h:223-236;
+ * the two agree whenever init is the op's identity or the op is Min/Max.) */
+int lcor_scan_op(int inclusive, int op, int dtype, const void *in, void *out, uint64_t n, const void *init)
+{
+    const size_t es = dtype_size(dtype);
+    if (!es || op < 0 || op > 2) return -1;
+    uint64_t carry = 0;
+    if (init) memcpy(&carry, init, es);
+    else init_value(op, dtype, &carry);
+    for (uint64_t i = 0; i < n; ++i) {
+        const char *x = (const char *)in + i * es;
+        char *o = (char *)out + i * es;
+        if (!inclusive) memcpy(o, &carry, es);
+        fold_any(op, dtype, x, 1, &carry);
+        if (inclusive) memcpy(o, &carry, es);
+    }
+    return 0;
+}
+
 int lcor_scan_f64(int inclusive, int dtype, const void *in, double *out, double *abs_prefix,
                   uint64_t n)
 {

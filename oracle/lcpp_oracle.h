@@ -26,6 +26,9 @@
  *                   reference KAT (max of squares of shuffled 0..4095)
  *   scan            numpy cumsum in the element type (wraparound), KATs
  *                   (ones -> i / i+1), look-back KAT (102400 tiles)
+ *   scan with op    numpy cumsum / minimum.accumulate / maximum.accumulate
+ *                   with init prepended, init = identity == the Sum scan,
+ *                   constant input closed forms, planted mistakes
  *   radix sort      numpy stable argsort/sort, reversed-keys KAT, float KAT
  *                   (libstdc++ mt19937 inputs, std::sort golden), stability
  *                   checker (planted-mistake tests)
@@ -88,6 +91,7 @@ int lcor_reduce_transform(int op, int xf, int dtype, const void *in, uint64_t n,
 
 /* ---------------- scan ------------------------------------------------- */
 int lcor_scan(int inclusive, int dtype, const void *in, void *out, uint64_t n);
+int lcor_scan_op(int inclusive, int op, int dtype, const void *in, void *out, uint64_t n, const void *init);
 int lcor_scan_f64(int inclusive, int dtype, const void *in, double *out, double *abs_prefix,
                   uint64_t n);
 int lcor_scan_mt(int inclusive, int dtype, const void *in, void *out, uint64_t n, int nthreads);

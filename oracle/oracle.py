@@ -57,6 +57,7 @@ def lib() -> ctypes.CDLL:
             "lcor_reduce_arg": (i, [i, i, vp, u64, vp, ctypes.POINTER(u32)]),
             "lcor_reduce_transform": (i, [i, i, i, vp, u64, vp, vp]),
             "lcor_scan": (i, [i, i, vp, vp, u64]),
+            "lcor_scan_op": (i, [i, i, i, vp, vp, u64, vp]),
             "lcor_scan_f64": (i, [i, i, vp, vp, vp, u64]),
             "lcor_scan_mt": (i, [i, i, vp, vp, u64, i]),
             "lcor_lookback_kat": (i, [u32, i, vp, vp]),
@@ -181,6 +182,16 @@ def scan(a: np.ndarray, inclusive: bool, nthreads: int = 1) -> np.ndarray:
         _ok(lib().lcor_scan(int(inclusive), _code(a), _p(a), _p(out), a.size), "scan")
     else:
         _ok(lib().lcor_scan_mt(int(inclusive), _code(a), _p(a), _p(out), a.size, nthreads), "scan_mt")
+    return out
+
+
+def scan_op(a: np.ndarray, inclusive: bool, op: int, init=None) -> np.ndarray:
+    """ExclusiveScan / InclusiveScan: a left fold from init (None = the op's identity)."""
+    a = np.ascontiguousarray(a)
+    out = np.empty_like(a)
+    iv = np.array([init], dtype=a.dtype) if init is not None else None
+    _ok(lib().lcor_scan_op(int(inclusive), op, _code(a), _p(a), _p(out), a.size, _p(iv) if iv is not None else None),
+        "scan_op")
     return out
 
 

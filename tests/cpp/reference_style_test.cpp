@@ -160,6 +160,30 @@ void test_scan()
     expect(ok, "DeviceScan::Exclusive/InclusiveSum ones 2^k");
 
     ok = true;
+    for (int k = 0; k < 22 && ok; k += 3) {  // ExclusiveScan / InclusiveScan with an initial value
+        const size_t n = (size_t(1) << k) + 7;
+        std::vector<int> h(n);
+        for (size_t i = 0; i < n; ++i) h[i] = int((i * 2654435761u) % 1001) - 500;
+        DevBuf<int> in(h), ex(n), inc(n), mx(n);
+        Temp temp(DeviceScan<>::GetTempStorageBytes<int>(n));
+        scanner.ExclusiveScan(cmdlist, temp.view(), in.view(), ex.view(), n, SumOp{}, 1000);
+        const std::vector<int> he = ex.download(n);
+        scanner.InclusiveScan(cmdlist, temp.view(), in.view(), inc.view(), n, SumOp{}, -3);
+        const std::vector<int> hi = inc.download(n);
+        scanner.InclusiveScan(cmdlist, temp.view(), in.view(), mx.view(), n, MaxOp{}, 450);
+        const std::vector<int> hm = mx.download(n);
+        int run_ex = 1000, run_in = -3, run_mx = 450;
+        for (size_t i = 0; i < n && ok; ++i) {
+            ok = he[i] == run_ex;
+            run_ex += h[i];
+            run_in += h[i];
+            run_mx = std::max(run_mx, h[i]);
+            ok = ok && hi[i] == run_in && hm[i] == run_mx;
+        }
+    }
+    expect(ok, "DeviceScan::ExclusiveScan / InclusiveScan (SumOp, MaxOp) with initial_value");
+
+    ok = true;
     for (int k = 5; k < 21 && ok; ++k) {  // ExclusiveSumByKey: keys i / 100, ones -> i % 100
         const size_t n = size_t(1) << k;
         std::vector<int> keys(n);

@@ -1,5 +1,6 @@
-"""DeviceScan::ExclusiveSum/InclusiveSum on the GPU through the C ABI:
-integers bit-exact (wraparound) against the oracle, floats within
+"""DeviceScan::ExclusiveSum/InclusiveSum and ExclusiveScan/InclusiveScan
+(Sum/Min/Max with an initial value) on the GPU through the C ABI: integers
+bit-exact (wraparound) against the oracle, floats within
 |y_i - yhat_i| <= 1e-5 * sum_{j<=i}|x_j| of a float64 scan."""
 import numpy as np
 import pytest
@@ -155,3 +156,99 @@ def test_past_2p32_elements_ones(gpu, kind):
     del out, idx, o
     torch.cuda.empty_cache()
     assert ok
+
+
+# ------------------------------------------------------------------ ExclusiveScan / InclusiveScan (op, init)
+ALL_DTYPES = [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64]
+SCAN_OPS = {"sum": o.OP_SUM, "min": o.OP_MIN, "max": o.OP_MAX}
+
+
+def run_op(kind, d_in, n, dtype, op, init, pad=0):
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceScan
+
+    out = g.empty(n, dtype, pad=pad)
+    tmp = g.temp(DeviceScan.GetTempStorageBytes(np.dtype(dtype).name, n))
+    getattr(DeviceScan(), kind)(tmp, d_in, out, n, op, init)
+    return g.to_host(out)
+
+
+def op_init(dtype, op):
+    """An initial value that changes the results: inside the data's range for
+    Min/Max, far from zero for Sum."""
+    if np.dtype(dtype).kind == "f":
+        return {"sum": 1.0e4, "min": -20.0, "max": 20.0}[op]
+    info = np.iinfo(dtype)
+    return {"sum": int(info.max // 7), "min": int(info.min // 2 + info.max // 2), "max": int(info.max // 3)}[op]
+
+
+@pytest.mark.parametrize("dtype", ALL_DTYPES)
+@pytest.mark.parametrize("op", ["sum", "min", "max"])
+@pytest.mark.parametrize("n", [1, 8191, 8193, 16385, 20481, 24577, 3 * 20480 + 5, 100_003])
+@pytest.mark.parametrize("pad", [0, 1])
+def test_scan_op_init_vs_oracle(gpu, dtype, op, n, pad):
+    """Integers (and float Min/Max: no rounding) bit-exact against the
+    oracle; float sums within 1e-5 * (|init| + sum_{j<=i}|x_j|) of a float64
+    scan.  Ragged last tiles, misaligned pointers (pad = 1)."""
+    import gpu_util as g
+
+    a = g.random_array(dtype, n, seed=n + pad + len(op))
+    init = op_init(dtype, op)
+    log(f"scan op={op} init={init} {np.dtype(dtype).name} n={n} pad={pad}")
+    d = g.to_dev(a, pad=pad)
+    for kind, incl in (("ExclusiveScan", False), ("InclusiveScan", True)):
+        got = run_op(kind, d, n, dtype, op, init, pad=pad)
+        if np.dtype(dtype).kind == "f" and op == "sum":
+            ref, ab = o.scan_f64(a, incl)
+            err = np.abs(got.astype(np.float64) - (ref + init))
+            assert (err <= RTOL_SCAN * (ab + abs(init)) + 1e-30).all(), kind
+        elif np.dtype(dtype).kind == "f":
+            # Min/Max of -0.0 and +0.0 return either zero depending on the fold order
+            assert np.array_equal(got, o.scan_op(a, incl, SCAN_OPS[op], init)), kind
+        else:
+            assert got.tobytes() == o.scan_op(a, incl, SCAN_OPS[op], init).tobytes(), kind
+
+
+@pytest.mark.parametrize("kind", ["ExclusiveScan", "InclusiveScan"])
+def test_scan_op_identity_init_equals_sum_scan(gpu, kind):
+    """Sum with init 0 is ExclusiveSum / InclusiveSum, bit for bit (integers)."""
+    import gpu_util as g
+
+    n = 200_001
+    a = g.random_array(np.int64, n, seed=3)
+    d = g.to_dev(a)
+    got = run_op(kind, d, n, np.int64, "sum", 0)
+    assert (got == run(kind.replace("Scan", "Sum"), d, n, np.int64)).all()
+
+
+@pytest.mark.parametrize("op", ["min", "max"])
+def test_scan_op_full_size_u32(gpu, op):
+    """2^28 uint32 running Min / Max from an init inside the data's range,
+    against numpy's minimum / maximum.accumulate (with init prepended)."""
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    log(f"scan u32 inclusive {op} full 2^28")
+    d = datagen.keys_u32(n)
+    init = 0x7FFFFFFF
+    got = run_op("InclusiveScan", d, n, np.uint32, op, init)
+    h = g.to_host(d)
+    npop = np.minimum if op == "min" else np.maximum
+    ref = npop.accumulate(np.concatenate([np.array([init], np.uint32), h]), dtype=np.uint32)[1:]
+    assert (got == ref).all()
+
+
+def test_scan_op_sum_full_size_exclusive_with_init(gpu):
+    """2^28 uint32 in [0, 255] with init 2^32 - 5: wraps at once, bit-exact."""
+    import gpu_util as g
+    from lc_parallel_primitive_amd import datagen
+
+    n = 1 << 28
+    log("scan u32 exclusive sum init full 2^28")
+    d = datagen.u8_u32(n)
+    init = (1 << 32) - 5
+    got = run_op("ExclusiveScan", d, n, np.uint32, "sum", init)
+    h = g.to_host(d)
+    inc = np.cumsum(h, dtype=np.uint32) + np.uint32(init)
+    assert got[0] == init and (got[1:] == inc[:-1]).all()

@@ -192,6 +192,72 @@ def test_scan_f64_against_numpy():
     assert ex[0] == 0 and np.allclose(ex[1:], ref[:-1], atol=1e-9)
 
 
+SCAN_OPS = {o.OP_SUM: np.add, o.OP_MIN: np.minimum, o.OP_MAX: np.maximum}
+
+
+def np_scan_init(a, inclusive, npop, init):
+    """numpy's in-order accumulate over [init] + a: exclusive = all but the
+    last, inclusive = all but the first (np.add.accumulate wraps integers in
+    the element type and adds floats left to right)."""
+    acc = npop.accumulate(np.concatenate([np.array([init], a.dtype), a]), dtype=a.dtype)
+    return acc[1:] if inclusive else acc[:-1]
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64])
+@pytest.mark.parametrize("op", [o.OP_SUM, o.OP_MIN, o.OP_MAX])
+@pytest.mark.parametrize("inclusive", [False, True])
+def test_scan_op_init_vs_numpy_accumulate(dt, op, inclusive):
+    # DeviceScan::ExclusiveScan / InclusiveScan (device_scan.h:114-178)
+    rng = np.random.default_rng(op * 10 + inclusive)
+    n = 30_001
+    if np.dtype(dt).kind == "f":
+        a = (rng.standard_normal(n) * 1000).astype(dt)
+        init = dt(-123.25)
+    else:
+        info = np.iinfo(dt)
+        a = rng.integers(info.min, info.max, n, dtype=dt, endpoint=True)
+        init = dt(info.max // 3)
+    got = o.scan_op(a, inclusive, op, init)
+    ref = np_scan_init(a, inclusive, SCAN_OPS[op], init)
+    assert got.tobytes() == ref.tobytes()
+
+
+@pytest.mark.parametrize("inclusive", [False, True])
+def test_scan_op_identity_init_is_the_sum_scan_and_constant_closed_form(inclusive):
+    a = o.gen("reduce_i32", 10_007, 5)
+    assert (o.scan_op(a, inclusive, o.OP_SUM) == o.scan(a, inclusive)).all()
+    assert (o.scan_op(a, inclusive, o.OP_SUM, 0) == o.scan(a, inclusive)).all()
+    # constant input c with init z: exclusive z + i c, inclusive z + (i + 1) c (int64, no wrap)
+    c, z, n = np.int64(-7), np.int64(10**12), 5000
+    i = np.arange(n, dtype=np.int64)
+    got = o.scan_op(np.full(n, c), inclusive, o.OP_SUM, z)
+    assert (got == z + (i + inclusive) * c).all()
+    # Min from an init below every element stays at init; Max from lowest() is numpy's
+    assert (o.scan_op(a, inclusive, o.OP_MIN, np.int32(-2**31)) == -2**31).all()
+    assert (o.scan_op(a, True, o.OP_MAX) == np.maximum.accumulate(a)).all()
+
+
+def test_scan_op_planted_mistakes_are_caught():
+    """Plausible restatement mistakes, applied to the oracle's own output,
+    fail the numpy check: init dropped, init folded in twice (as the
+    reference's first tile does once per warp), exclusive / inclusive
+    shifted by one, min for max."""
+    a = o.gen("reduce_i32", 4096, 9).astype(np.int64)
+    z = np.int64(1000)
+    ref_ex = np_scan_init(a, False, np.add, z)
+    ref_in = np_scan_init(a, True, np.add, z)
+    assert (o.scan_op(a, False, o.OP_SUM, z) == ref_ex).all()
+    planted = {
+        "init dropped": o.scan_op(a, False, o.OP_SUM, z) - z,
+        "init twice": o.scan_op(a, False, o.OP_SUM, z) + z,
+        "inclusive for exclusive": o.scan_op(a, True, o.OP_SUM, z),
+    }
+    for what, bad in planted.items():
+        assert not (bad == ref_ex).all(), what
+    assert not (o.scan_op(a, True, o.OP_MIN, z) == np_scan_init(a, True, np.maximum, z)).all()
+    assert not (o.scan_op(a, False, o.OP_SUM, z) == ref_in).all()
+
+
 def test_lookback_kat_102400_tiles():
     # decoupled_look_back.cpp:57-174: aggregate 1 per tile -> exclusive i, inclusive i+1
     ex, inc = o.lookback_kat(102400, 8)
