@@ -1,5 +1,5 @@
 """Seeded randomized parity cases for every primitive: random sizes (1 to
-2^20, log-uniform), integer dtypes, value distributions (uniform, few
+2^20, log-uniform, plus 4 cases per group between 2^22 and 2^26), integer dtypes, value distributions (uniform, few
 distinct, AND-of-3, constant), sort directions, run lengths and segment
 layouts (tiling, random order, random windows with overlaps, gaps and
 inverted ranges).  Integer data, so every result is exact against the
@@ -14,9 +14,17 @@ from oracle import oracle as o
 pytestmark = pytest.mark.gpu
 
 INT_DTYPES = [np.int32, np.uint32, np.int64, np.uint64]
-# Sizes are log-uniform in [2^LOG2_RANGE[0], 2^LOG2_RANGE[1]); the long-run
-# driver (tests/random_sweep.py) widens the range.
+# Sizes are log-uniform in [2^LOG2_RANGE[0], 2^LOG2_RANGE[1]); every group
+# also runs LARGE_CASES seeds in LOG2_LARGE (the regime where a wrapped gather
+# offset once showed: ~3e7 elements).
 LOG2_RANGE = (0, 20)
+LOG2_LARGE = (22, 26)
+LARGE_CASES = 4
+
+
+def cases(n_small):
+    """(seed, log2 size range) pairs: n_small small cases, then the large ones."""
+    return [(s, LOG2_RANGE) for s in range(n_small)] + [(100 + s, LOG2_LARGE) for s in range(LARGE_CASES)]
 
 
 def values(rng, dt, n, kind):
@@ -34,18 +42,18 @@ def values(rng, dt, n, kind):
     return np.full(n, rng.integers(info.min, info.max, dtype=dt, endpoint=True), dtype=dt)
 
 
-def case_params(seed):
+def case_params(seed, log2_range=LOG2_RANGE):
     rng = np.random.default_rng(seed)
-    n = int(np.exp(rng.uniform(LOG2_RANGE[0] * np.log(2), LOG2_RANGE[1] * np.log(2))))
+    n = int(np.exp(rng.uniform(log2_range[0] * np.log(2), log2_range[1] * np.log(2))))
     return rng, n, INT_DTYPES[rng.integers(0, 4)], int(rng.integers(0, 4))
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_reduce_and_scan(gpu, seed):
+@pytest.mark.parametrize("seed,lr", cases(24))
+def test_random_reduce_and_scan(gpu, seed, lr):
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceReduce, DeviceScan
 
-    rng, n, dt, kind = case_params(1000 + seed)
+    rng, n, dt, kind = case_params(1000 + seed, lr)
     a = values(rng, dt, n, kind)
     log(f"random reduce/scan seed={seed} n={n} {np.dtype(dt).name} kind={kind}")
     d = g.to_dev(a)
@@ -67,14 +75,20 @@ def test_random_reduce_and_scan(gpu, seed):
     for inclusive in (False, True):
         (s.InclusiveSum if inclusive else s.ExclusiveSum)(tmps, d, so, n)
         assert (g.to_host(so) == o.scan(a, inclusive)).all(), inclusive
+    op = ["sum", "min", "max"][seed % 3]
+    init = values(rng, dt, 1, 0)[0]
+    for inclusive in (False, True):
+        (s.InclusiveScan if inclusive else s.ExclusiveScan)(tmps, d, so, n, op, init)
+        ref = o.scan_op(a, inclusive, {"sum": o.OP_SUM, "min": o.OP_MIN, "max": o.OP_MAX}[op], init)
+        assert (g.to_host(so) == ref).all(), (op, inclusive)
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_sorts(gpu, seed):
+@pytest.mark.parametrize("seed,lr", cases(24))
+def test_random_sorts(gpu, seed, lr):
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceRadixSort
 
-    rng, n, dt, kind = case_params(2000 + seed)
+    rng, n, dt, kind = case_params(2000 + seed, lr)
     a = values(rng, dt, n, kind)
     desc = bool(rng.integers(0, 2))
     vdt = [np.uint32, np.uint64][rng.integers(0, 2)]
@@ -92,14 +106,14 @@ def test_random_sorts(gpu, seed):
     assert (g.to_host(ko) == rk).all() and (g.to_host(vo) == rv).all()
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_by_key(gpu, seed):
+@pytest.mark.parametrize("seed,lr", cases(24))
+def test_random_by_key(gpu, seed, lr):
     import torch
 
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceReduce, DeviceScan
 
-    rng, n, dt, kind = case_params(3000 + seed)
+    rng, n, dt, kind = case_params(3000 + seed, lr)
     run = int(rng.integers(1, 400))
     keys = np.repeat(rng.integers(0, 4, size=n // run + 1), run)[:n].astype(dt)
     vals = values(rng, np.int32, n, 1)
@@ -121,12 +135,12 @@ def test_random_by_key(gpu, seed):
     assert m == rk.size and (g.to_host(uk)[:m] == rk).all() and (g.to_host(ag)[:m] == rv).all()
 
 
-@pytest.mark.parametrize("seed", range(36))
-def test_random_segments(gpu, seed):
+@pytest.mark.parametrize("seed,lr", cases(36))
+def test_random_segments(gpu, seed, lr):
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceSegmentReduce
 
-    rng, n, dt, kind = case_params(4000 + seed)
+    rng, n, dt, kind = case_params(4000 + seed, lr)
     a = values(rng, dt, n, kind)
     S = max(1, int(rng.integers(1, 1 + max(1, n // int(rng.integers(1, 200))))))
     layout = seed % 3
@@ -153,8 +167,8 @@ def test_random_segments(gpu, seed):
         assert (g.to_host(out) == ev).all() and (g.to_host(idx) == ei).all(), nm
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_misaligned_and_variants(gpu, seed):
+@pytest.mark.parametrize("seed,lr", cases(24))
+def test_random_misaligned_and_variants(gpu, seed, lr):
     """Pointers 0-3 elements off their 16-byte alignment (the element-wise
     load paths), transform reduce, scan-by-key with Min/Max/Sum and an
     initial value over 32- or 64-bit values, ReduceByKey with 64-bit values,
@@ -164,7 +178,7 @@ def test_random_misaligned_and_variants(gpu, seed):
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceReduce, DeviceScan, DeviceRadixSort, DeviceSegmentReduce
 
-    rng, n, dt, kind = case_params(5000 + seed)
+    rng, n, dt, kind = case_params(5000 + seed, lr)
     pad = int(rng.integers(0, 4))
     a = values(rng, dt, n, kind)
     ops = {"sum": o.OP_SUM, "min": o.OP_MIN, "max": o.OP_MAX}
@@ -216,15 +230,15 @@ def test_random_misaligned_and_variants(gpu, seed):
     assert (g.to_host(sout) == ev).all() and (g.to_host(sidx) == ei).all()
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_floats(gpu, seed):
+@pytest.mark.parametrize("seed,lr", cases(24))
+def test_random_floats(gpu, seed, lr):
     """float32 / float64 data (normal at a random scale, few distinct values,
     +-0, +-inf): sorts and Min/Max/Arg* exact against the oracle, sums and
     scans within 1e-5 * sum|x| of float64 (finite data)."""
     import gpu_util as g
     from lc_parallel_primitive_amd import DeviceReduce, DeviceScan, DeviceRadixSort, DeviceSegmentReduce
 
-    rng, n, _, kind = case_params(6000 + seed)
+    rng, n, _, kind = case_params(6000 + seed, lr)
     dt = [np.float32, np.float64][seed % 2]
     if kind == 0:
         a = rng.standard_normal(n) * 10 ** rng.uniform(-3, 3)

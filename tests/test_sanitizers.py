@@ -62,4 +62,7 @@ def test_capi_host_asan_ubsan():
     _make("_san/capi_asan", 900)
     r = _run("capi_asan", env={"ASAN_OPTIONS": "detect_leaks=0"})
     assert r.returncode == 0, r.stdout + r.stderr[-4000:]
-    assert "capi_args: OK" in r.stdout or "skipped" in r.stdout
+    if "capi_args: OK" not in r.stdout:
+        # capi_args sweeps the argument checks only where no GPU is visible
+        assert "skipped" in r.stdout, r.stdout
+        pytest.skip("capi_args: a GPU is visible, so the argument sweep did not run")
