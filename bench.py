@@ -103,9 +103,25 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps  # ms per step
 
+    def event_floor_ms(reps=50):
+        """Median elapsed time of an empty pair of HIP events recorded back to back
+        on the stream: what an event pair adds to the kernel it brackets."""
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return statistics.median(ts)
+
+    floor_ms = event_floor_ms()
+
     def kernel_ms(call, steps, name):
         """Average device duration of kernel `name` over `steps` calls (HIP events
-        recorded by the library around each launch, on the launch stream)."""
+        recorded by the library around each launch, on the launch stream), less
+        the empty event-pair floor.  Returns (corrected ms, raw ms, launches,
+        {kernel: (launches, total ms)})."""
         lcpp.profile_enable()
         for _ in range(steps):
             call()
@@ -113,7 +129,8 @@ def main():
         rec = lcpp.profile_read()
         lcpp.profile_disable()
         launches, total = rec[name]
-        return total / launches, launches, rec
+        raw = total / launches
+        return max(raw - floor_ms, 0.0), raw, launches, rec
 
     U32, F32, I32, U64 = 1, 2, 0, 4
     chk = lcpp._capi.check
@@ -158,10 +175,13 @@ def main():
     ms = timed(sort_call, args.steps, args.warmup)
     gkeys = n / (ms * 1e-3) / 1e9
     progress(f"SortKeys u32 2^28: {ms:.4f} ms/step, {gkeys:.2f} Gkeys/s")
-    pass_ms, pass_launches, rec = kernel_ms(sort_call, max(2, args.steps // 4), "rs_onesweep")
+    pass_ms, pass_raw_ms, pass_launches, rec = kernel_ms(sort_call, max(2, args.steps // 4), "rs_onesweep")
     pass_bytes = 8 * n  # read 4N + write 4N per onesweep pass (algorithmic)
     achieved = pass_bytes / (pass_ms * 1e-3) / 1e9
-    breakdown = {k: round(v[1] / v[0] * 1e3, 2) for k, v in rec.items()}  # us per launch
+    breakdown = {k: round((v[1] / v[0] - floor_ms) * 1e3, 2) for k, v in rec.items()}  # us per launch
+    rp = ctypes.c_int(0)
+    chk(L.lcpp_radix_sort_rank_path(ctypes.byref(rp)), "rank_path")
+    rank_path = {1: "lds_atomic (lane-order probe passed)", 2: "ballot_match"}[rp.value]
     del temp, out
 
     result = {
@@ -184,6 +204,8 @@ def main():
             "algorithmic_bytes_per_sort": 36 * n,
             "sort_roofline_frac": round(36 * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "us_per_launch": breakdown,
+            "event_floor_us": round(floor_ms * 1e3, 2),
+            "rank_path": rank_path,
         },
         "roofline": {
             "bound": "hbm",
@@ -196,6 +218,7 @@ def main():
             "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated: profiles/rs_onesweep_u32_2p28_hbm_bytes.txt",
             "bytes_per_launch": pass_bytes,
             "avg_launch_us": round(pass_ms * 1e3, 2),
+            "avg_launch_us_raw_events": round(pass_raw_ms * 1e3, 2),
             "launches": pass_launches,
         },
     }
@@ -223,11 +246,12 @@ def main():
 
         def add(name, unit_bytes, call, steps, kname, items=None, cpu=None, flushed=False, note=None):
             t = flushed_ms(call, steps) if flushed else timed(call, steps, 2)
-            kms, _, _ = kernel_ms(call, max(2, steps // 2), kname)
+            kms, kraw, _, _ = kernel_ms(call, max(2, steps // 2), kname)
             gbs = unit_bytes / (t * 1e-3) / 1e9
             entry = {"workload": name, "ms": round(t, 4), "GB/s": round(gbs, 1),
                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                     "dominant_kernel": kname, "kernel_us": round(kms * 1e3, 2)}
+                     "dominant_kernel": kname, "kernel_us": round(kms * 1e3, 2),
+                     "kernel_us_raw_events": round(kraw * 1e3, 2)}
             if flushed:
                 tu = timed(call, steps, 2)
                 entry["mall"] = "flushed (1 GiB written before each timed call)"
@@ -299,6 +323,23 @@ def main():
                                                    ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(ko.data_ptr()), n,
                                                    sp), "sort"), 10, "rs_onesweep", items=n,
                 cpu=lambda: cpu_sort("keys_u32_and3", n))
+            del k, ko, t1
+        if want("sort_match"):
+            # the headline sort with the ballot-match ranking forced (the fallback
+            # the lane-order probe would select)
+            n = 1 << 28
+            k = datagen.keys_u32(n)
+            ko = torch.empty_like(k)
+            tb = tmp_bytes(L.lcpp_radix_sort_keys_temp_bytes, U32, n)
+            t1 = torch.empty(tb, dtype=torch.uint8, device="cuda")
+            chk(L.lcpp_test_set_sort_rank_path(2), "rank path")
+            try:
+                add("DeviceRadixSort::SortKeys uint32 N=2^28 uniform, ballot-match ranking forced", 36 * n,
+                    lambda: chk(L.lcpp_radix_sort_keys(U32, ctypes.c_void_p(t1.data_ptr()), tb,
+                                                       ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(ko.data_ptr()),
+                                                       n, sp), "sort"), 10, "rs_onesweep", items=n)
+            finally:
+                chk(L.lcpp_test_set_sort_rank_path(0), "rank path")
             del k, ko, t1
         if want("pairs"):
             n = 1 << 27

@@ -263,6 +263,21 @@ int lcpp_radix_sort_pairs_descending(lcpp_dtype k, lcpp_dtype v, void *temp, siz
                                      const void *keys_in, void *keys_out, const void *vals_in,
                                      void *vals_out, uint64_t n, void *stream);
 
+/* No counterpart in the reference (whose MatchAny ranking, common/utils.h:273-324 and
+ * block/block_radix_rank.h:254-280, has no alternative).  The onesweep ranks keys either with
+ * returning LDS atomics, which are stable only if the LDS serves the lanes of one instruction
+ * that hit one address in lane order (gfx950 does; no ISA document promises it), or with a
+ * ballot match, stable by construction.  The first sort on each device runs an in-bounds
+ * probe of that lane order (~10 us, synchronizes a private stream) and takes the atomic path
+ * only if the probe sees no violation.  A first sort made while its stream is being captured
+ * into a graph takes the match path.  Writes the path the sorts on the current device use:
+ * 1 = LDS atomics, 2 = ballot match (running the probe if it has not run on this device). */
+int lcpp_radix_sort_rank_path(int *path);
+/* Test hook, process-wide: 0 = the probe's choice (default), 1 = force the LDS-atomic
+ * ranking, 2 = force the ballot-match ranking.  Calls running concurrently see the same
+ * setting. */
+int lcpp_test_set_sort_rank_path(int mode);
+
 /* ---------------------------------------------------------------------
  * DeviceSegmentReduce — device/device_segment_reduce.h
  * ------------------------------------------------------------------- */

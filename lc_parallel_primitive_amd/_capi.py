@@ -48,6 +48,8 @@ SIGNATURES = {
     "lcpp_radix_sort_pairs": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp, _u64, _vp]),
     "lcpp_radix_sort_keys_descending": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _u64, _vp]),
     "lcpp_radix_sort_pairs_descending": (_i, [_i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp, _u64, _vp]),
+    "lcpp_radix_sort_rank_path": (_i, [ctypes.POINTER(_i)]),
+    "lcpp_test_set_sort_rank_path": (_i, [_i]),
     "lcpp_scan_by_key_temp_bytes": (_i, [_i, _i, _u64, _c_size_p]),
     "lcpp_scan_exclusive_by_key": (_i, [_i, _i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, _vp, _vp]),
     "lcpp_scan_inclusive_by_key": (_i, [_i, _i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, _vp, _vp]),

@@ -33,6 +33,21 @@ __device__ __forceinline__ uint32_t mask_rank(uint64_t mask)
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+// Match-any over an 8-bit value: the lanes of the wave whose low 8 bits of v
+// equal this lane's (one ballot per bit; common/utils.h:273-324, MatchAny<8>,
+// does the same over 32 lanes).  Every lane of the wave must be active.
+__device__ __forceinline__ uint64_t match_any8(uint32_t v)
+{
+    uint64_t peers = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const bool bit = (v >> b) & 1u;
+        const uint64_t ones = ballot(bit);
+        peers &= bit ? ones : ~ones;
+    }
+    return peers;
+}
+
 // ---------------------------------------------------------------- ops
 struct SumOp {
     template <class T>

@@ -19,10 +19,10 @@
 //    arrival counter.
 //  * launch 1 "rs_histogram": one 1024-thread workgroup per CU streams a
 //    contiguous chunk of keys and counts all P = sizeof(K) 8-bit digits at
-//    once into an LDS table with 32 (16 for 8-byte keys) lane-private copies
-//    of every counter, so that equal digits in one wave (skewed or constant
-//    key bytes) never hit one LDS address; flushed with one global atomic per
-//    non-zero bin.  It also zeroes the look-back state of pass 0.  The last
+//    once into an LDS table in which every lane of a wave counts into its
+//    own column (16 lane copies of every counter for 8-byte keys), so that
+//    equal digits in one wave (skewed or constant key bytes) never hit one
+//    LDS address; flushed with one global atomic per non-zero bin.  It also zeroes the look-back state of pass 0.  The last
 //    workgroup to finish (the arrival counter, release/acquire at agent
 //    scope) finds each pass's hot digit and plans the passes from the
 //    finished histograms (below).
@@ -72,6 +72,8 @@
 //    does; equal keys keep their input order.
 //  * Keys-only sorts reserve no value scratch (the reference reserves N
 //    values it never uses, device_radix_sort.h:118-122).
+#include <mutex>
+
 #include "common.hpp"
 
 namespace lcpp {
@@ -261,23 +263,38 @@ __device__ void rs_make_plan(const uint32_t *bins, uint32_t passes, uint64_t n, 
 }
 
 // ------------------------------------------------------------------ histogram
+// Counter layouts in LDS (128 KiB either way):
+//  * 4-byte keys, lane columns: lane l of every wave owns column l of a
+//    [P][128][64] table of 32-bit words, each holding the 16-bit counters of
+//    digits d and d + 128 (d < 128) of one pass.  A wave's counting atomic
+//    touches 64 distinct words in 64 distinct banks whatever the digits are
+//    (no bank conflicts, no same-address lanes).  A column counts at most 1/64
+//    of the keys a workgroup has seen since its last flush, so the table is
+//    flushed every kHistRoundSteps loop steps (4,177,920 keys < 64 x 65536).
+//  * 8-byte keys: [P][256][16], lane l counting into copy l % 16.
+template <class UK>
+constexpr bool hist_lane_columns()
+{
+    return sizeof(UK) == 4;
+}
 template <class UK>
 constexpr int hist_copies()
 {
-    return sizeof(UK) == 4 ? 32 : 16;  // 128 KB of LDS either way
+    return 16;  // 8-byte keys
 }
-// Dynamic LDS: the counter table [P][256][C], then 17 words of planning state
-// for the last workgroup (the kernel has no static LDS).
+// Dynamic LDS: the counter table, then 17 words of planning state for the
+// last workgroup (the kernel has no static LDS).
 template <class UK>
 constexpr size_t hist_table_words()
 {
-    return sizeof(UK) * kRadix * hist_copies<UK>();
+    return hist_lane_columns<UK>() ? sizeof(UK) * (kRadix / 2) * kWave : sizeof(UK) * kRadix * hist_copies<UK>();
 }
 template <class UK>
 constexpr size_t hist_lds_bytes()
 {
     return (hist_table_words<UK>() + 17) * 4;
 }
+constexpr uint64_t kHistRoundSteps = 255;  // loop steps between flushes of the lane-column table
 
 template <class UK, int KIND, bool DESC>
 __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
@@ -286,12 +303,14 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     uint32_t *__restrict__ hot, uint32_t *__restrict__ plan)
 {
     constexpr int P = sizeof(UK);
+    constexpr bool LC = hist_lane_columns<UK>();
     constexpr int C = hist_copies<UK>();
-    extern __shared__ uint32_t s_hist[];  // [P][256][C], then s_last, s_trivial[16]
+    constexpr uint32_t W = (uint32_t)hist_table_words<UK>();
+    extern __shared__ uint32_t s_hist[];  // the counter table, then s_last, s_trivial[16]
     const uint32_t tid = threadIdx.x;
-    const uint32_t copy = lane_id() % C;
-    uint32_t *s_last = s_hist + hist_table_words<UK>(), *s_trivial = s_last + 1;
-    for (uint32_t i = tid; i < (uint32_t)(P * kRadix * C); i += kHistBlock) s_hist[i] = 0;
+    const uint32_t lane = lane_id();
+    uint32_t *s_last = s_hist + W, *s_trivial = s_last + 1;
+    for (uint32_t i = tid; i < W; i += kHistBlock) s_hist[i] = 0;
     // zero the look-back state of pass 0 (before the counts, so that the
     // release below covers these stores as well)
     const uint64_t stride = (uint64_t)gridDim.x * kHistBlock;
@@ -304,38 +323,68 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     auto count = [&](UK raw) {
         const UK tk = sort_key<UK, KIND, DESC>(raw);
 #pragma unroll
-        for (int p = 0; p < P; ++p)
-            atomicAdd(&s_hist[((uint32_t)p * kRadix + digit_of<UK, KIND, DESC>(tk, p * kRadixBits)) * C + copy], 1u);
+        for (int p = 0; p < P; ++p) {
+            const uint32_t dg = digit_of<UK, KIND, DESC>(tk, p * kRadixBits);
+            if constexpr (LC)
+                atomicAdd(&s_hist[(((uint32_t)p * (kRadix / 2) + (dg & 127u)) << 6) + lane], dg & 128u ? 0x10000u : 1u);
+            else
+                atomicAdd(&s_hist[((uint32_t)p * kRadix + dg) * C + lane % C], 1u);
+        }
+    };
+    // one global add per non-zero bin (the sum of its counters); the table is
+    // zeroed again when more keys follow
+    auto flush = [&](bool more) {
+        __syncthreads();
+        for (uint32_t i = tid; i < (uint32_t)(P * kRadix); i += kHistBlock) {
+            uint32_t c = 0;
+            if constexpr (LC) {
+                const uint32_t d = i % kRadix;
+                const uint32_t *col = s_hist + ((i / kRadix * (kRadix / 2) + (d & 127u)) << 6);
+                const uint32_t sh = (d >> 7) * 16u;
+                // threads of a wave start at different columns: no bank conflicts
+#pragma unroll 8
+                for (uint32_t k = 0; k < (uint32_t)kWave; ++k) c += (col[(k + d) & 63u] >> sh) & 0xFFFFu;
+            } else {
+#pragma unroll 8
+                for (int k = 0; k < C; ++k) c += s_hist[i * C + k];
+            }
+            if (c) __hip_atomic_fetch_add(&bins[i], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (more) {
+            __syncthreads();
+            for (uint32_t i = tid; i < W; i += kHistBlock) s_hist[i] = 0;
+        }
     };
     constexpr uint64_t V = 16 / sizeof(UK);
     constexpr int kVecs = 4;
     constexpr uint64_t step = (uint64_t)kHistBlock * V * kVecs;
-    uint64_t tail = b0;
-    if ((reinterpret_cast<uintptr_t>(keys) & 15) == 0) {
-        const uint64_t full_end = b0 + (b1 - b0) / step * step;
-        for (uint64_t t = b0; t < full_end; t += step) {
-            u32x4 v[kVecs];
+    const bool vec = (reinterpret_cast<uintptr_t>(keys) & 15) == 0;
+    // rounds of whole steps (every round but the last is a multiple of the step)
+    const uint64_t round_len = LC ? kHistRoundSteps * step : ~0ull;
+    for (uint64_t r0 = b0; r0 < b1;) {
+        const uint64_t r1 = b1 - r0 > round_len ? r0 + round_len : b1;
+        uint64_t tail = r0;
+        if (vec) {
+            const uint64_t full_end = r0 + (r1 - r0) / step * step;
+            for (uint64_t t = r0; t < full_end; t += step) {
+                u32x4 v[kVecs];
 #pragma unroll
-            for (int i = 0; i < kVecs; ++i) v[i] = ld16_nt(keys + t + ((uint64_t)i * kHistBlock + tid) * V);
+                for (int i = 0; i < kVecs; ++i) v[i] = ld16_nt(keys + t + ((uint64_t)i * kHistBlock + tid) * V);
 #pragma unroll
-            for (int i = 0; i < kVecs; ++i) {
-                UK e[V];
-                unpack16<UK>(v[i], e);
+                for (int i = 0; i < kVecs; ++i) {
+                    UK e[V];
+                    unpack16<UK>(v[i], e);
 #pragma unroll
-                for (int j = 0; j < (int)V; ++j) count(e[j]);
+                    for (int j = 0; j < (int)V; ++j) count(e[j]);
+                }
             }
+            tail = full_end;
         }
-        tail = full_end;
+        for (uint64_t i = tail + tid; i < r1; i += kHistBlock) count(keys[i]);
+        r0 = r1;
+        if (r0 < b1) flush(true);
     }
-    for (uint64_t i = tail + tid; i < b1; i += kHistBlock) count(keys[i]);
-    __syncthreads();
-    // one global add per non-zero bin (sum of the lane copies)
-    for (uint32_t i = tid; i < (uint32_t)(P * kRadix); i += kHistBlock) {
-        uint32_t c = 0;
-#pragma unroll 8
-        for (int k = 0; k < C; ++k) c += s_hist[i * C + k];
-        if (c) __hip_atomic_fetch_add(&bins[i], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    flush(false);
 
     // The last workgroup to arrive plans the passes (hot digits, skipped
     // passes, buffer routing) from the finished bins: every workgroup's adds
@@ -420,7 +469,9 @@ __device__ __forceinline__ uint32_t set_half16(uint32_t w, int hi, uint32_t v)
     return hi ? (w & 0xFFFFu) | (v << 16) : (w & 0xFFFF0000u) | v;
 }
 
-template <int IPT, class UK, class UV, int KIND, bool PAIRS, bool DESC>
+// MATCH: rank by ballot match (stable by construction) instead of relying on
+// the lane order of same-address LDS atomics (rs_rank_path picks one).
+template <int IPT, class UK, class UV, int KIND, bool PAIRS, bool DESC, bool MATCH>
 __global__ __launch_bounds__(kOsBlock)
 __attribute__((amdgpu_waves_per_eu(os_waves_per_eu<UK, UV, PAIRS>(), os_waves_per_eu<UK, UV, PAIRS>())))
 void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const uint32_t *__restrict__ bins,
@@ -493,8 +544,13 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();  // counters zeroed
 
-    // ---- stable rank within (wave, digit): lane-ordered LDS atomics; two
-    // 16-bit ranks per register
+    // ---- stable rank within (wave, digit); two 16-bit ranks per register.
+    // Atomic path: lane-ordered LDS atomics.  MATCH path: the lanes holding
+    // one digit (match_any8) are ranked by position among them on a base that
+    // their lowest lane fetches with one atomic add of their number, so no
+    // two lanes of an instruction touch one counter
+    // (block/block_radix_rank.h:254-280, ComputeRanksItem<WARP_MATCH_ANY>).
+    // The wave's LDS instructions complete in program order either way.
     uint32_t rank2[IPT / 2];
     uint32_t *cnt = sm.cnt[wave];
     // Lanes holding the pass's hot digit (skewed inputs: up to a third of the
@@ -504,6 +560,13 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     // separate loop for passes without a hot digit measured no faster.)
     const uint32_t hot = hot_digit;
     auto rank_of = [&](uint32_t dd) -> uint32_t {
+        if constexpr (MATCH) {
+            const uint64_t peers = match_any8(dd);
+            const uint32_t below = mask_rank(peers);
+            uint32_t b = 0;
+            if (below == 0) b = atomicAdd(&cnt[dd], (uint32_t)__builtin_popcountll(peers));
+            return (uint32_t)__shfl((int)b, (int)__builtin_ctzll(peers)) + below;
+        }
         const bool in_hot = dd == hot;
         const uint64_t m = ballot(in_hot);
         const uint32_t leader = m ? (uint32_t)__builtin_ctzll(m) : (uint32_t)kWave;
@@ -519,7 +582,8 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
         const uint32_t r0 = rank_of(digit_of<UK, KIND, DESC>(tk[u], shift));
         const uint32_t r1 = rank_of(digit_of<UK, KIND, DESC>(tk[u + 1], shift));
         rank2[u / 2] = r0 | (r1 << 16);
-        if ((u & 7) == 6) __builtin_amdgcn_sched_barrier(0);
+        // (match path: one pair at a time keeps its ballot masks from spilling)
+        if (MATCH || (u & 7) == 6) __builtin_amdgcn_sched_barrier(0);
     }
     // Opaque copies: the counter addresses are recomputed after the barrier
     // (two VALU ops) instead of being kept live (one register per key).
@@ -739,6 +803,161 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     return L;
 }
 
+// ------------------------------------------------------------------ rank path
+// The atomic ranking path gives stable ranks only if the LDS serves the lanes
+// of one returning atomic that hit one address in lane order.  That is how
+// gfx950 behaves, but no ISA document promises it, so the first sort on each
+// device runs a probe (~10 us, in bounds): 1024 waves x 32 instructions of
+// same-address LDS atomics over uniform, hot, constant and two-value digits
+// with varying addends, every result checked against the lane-order value.
+// Any violation selects the match path, which is stable by construction.
+constexpr int kRankAtomic = 1, kRankMatch = 2;
+constexpr uint32_t kProbeBlocks = 256, kProbeRounds = 32;
+
+// splitmix64's output function (Vigna): the probe's digits
+__device__ __forceinline__ uint64_t probe_mix(uint64_t x)
+{
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// Four waves per workgroup, each on its own 256 counters; pattern = block & 3.
+// *violations += lanes whose atomic result differs from the counter's value
+// before the instruction plus the addends of the lower lanes with its digit.
+// Every LDS index is below 256 per wave.
+__global__ __launch_bounds__(256) void rs_lane_order_probe_kernel(uint32_t rounds, unsigned long long *violations)
+{
+    __shared__ uint32_t cnt[4][kRadix];
+    __shared__ uint32_t before[4][kRadix];
+    const uint32_t lane = lane_id(), w = threadIdx.x / kWave, pattern = blockIdx.x & 3u;
+    for (uint32_t i = lane; i < (uint32_t)kRadix; i += kWave) cnt[w][i] = 0;
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t wid = (uint64_t)blockIdx.x * 4 + w;
+    uint32_t bad = 0;
+    for (uint32_t r = 0; r < rounds; ++r) {
+        const uint64_t h = probe_mix((wid * rounds + r) * kWave + lane);
+        uint32_t d;
+        if (pattern == 0) d = (uint32_t)h & 255u;
+        else if (pattern == 1) d = (h >> 40) % 3 == 0 ? 0u : (uint32_t)h & 255u;
+        else if (pattern == 2) d = (uint32_t)probe_mix(wid * rounds + r) & 255u;
+        else d = (h >> 12) & 1u ? 17u : 200u;
+        const uint32_t add = 1u + (uint32_t)((h >> 20) & 3u);
+        for (uint32_t i = lane; i < (uint32_t)kRadix; i += kWave) before[w][i] = cnt[w][i];
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t got = atomicAdd(&cnt[w][d], add);
+        uint32_t lower = 0;
+        for (int j = 0; j < kWave; ++j) {
+            const uint32_t dj = (uint32_t)__builtin_amdgcn_readlane((int)d, j);
+            const uint32_t aj = (uint32_t)__builtin_amdgcn_readlane((int)add, j);
+            lower += ((uint32_t)j < lane && dj == d) ? aj : 0u;
+        }
+        bad += got != before[w][d] + lower ? 1u : 0u;
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (bad) atomicAdd(violations, (unsigned long long)bad);
+}
+
+}  // namespace
+}  // namespace lcpp
+
+// The probe's violation counter (one per GPU the library runs on).  Host code
+// uses the address hipGetSymbolAddress returns, never the name.
+static __device__ __align__(8) unsigned long long rs_probe_violations;
+
+namespace lcpp {
+namespace {
+
+std::atomic<int> g_rank_force{0};  // lcpp_test_set_sort_rank_path
+std::mutex g_probe_mu;
+DeviceCache g_rank_cache;
+
+// Runs the probe on a private stream and waits for it: kRankAtomic when no
+// violation was seen, kRankMatch otherwise, -1 when a HIP call failed.
+int rs_run_probe()
+{
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(rs_probe_violations)) != hipSuccess || !addr) return -1;
+    hipStream_t ps = nullptr;
+    if (hipStreamCreateWithFlags(&ps, hipStreamNonBlocking) != hipSuccess) return -1;
+    unsigned long long v = ~0ull;
+    rs_init_kernel<<<1, 256, 0, ps>>>(static_cast<uint32_t *>(addr), 2);
+    rs_lane_order_probe_kernel<<<kProbeBlocks, 256, 0, ps>>>(kProbeRounds, static_cast<unsigned long long *>(addr));
+    const bool ok = hipGetLastError() == hipSuccess &&
+                    hipMemcpyAsync(&v, addr, sizeof(v), hipMemcpyDeviceToHost, ps) == hipSuccess &&
+                    hipStreamSynchronize(ps) == hipSuccess;
+    (void)hipStreamDestroy(ps);
+    if (!ok) return -1;
+    return v == 0 ? kRankAtomic : kRankMatch;
+}
+
+// The ranking path of the sorts on the current device.  The probe runs once
+// per device, on its first sort.  A first sort made while its stream is being
+// captured into a graph cannot wait for a probe: it takes the match path
+// (correct everywhere) and the probe runs on a later call.
+int rs_rank_path(hipStream_t s)
+{
+    const int forced = g_rank_force.load(std::memory_order_relaxed);
+    if (forced) return forced;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return kRankMatch;
+    int x = g_rank_cache.v[dev].load(std::memory_order_relaxed);
+    if (x) return x;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return kRankMatch;
+    }
+    std::lock_guard<std::mutex> lk(g_probe_mu);
+    x = g_rank_cache.v[dev].load(std::memory_order_relaxed);
+    if (x) return x;
+    x = rs_run_probe();
+    if (x < 0) {
+        (void)hipGetLastError();  // the probe's own failure; this call takes the match path
+        return kRankMatch;
+    }
+    g_rank_cache.v[dev].store(x, std::memory_order_relaxed);
+    return x;
+}
+
+// XCD run length of one onesweep instantiation: 8R <= half the workgroups
+// resident at once.  log2(R) + 1, or -1 when the occupancy query fails.
+template <int IPT, class UK, class UV, int KIND, bool PAIRS, bool DESC, bool MATCH>
+int rs_log_run()
+{
+    static DeviceCache run_cache;
+    return device_cached(run_cache, [] {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void *>(&rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC, MATCH>),
+                kOsBlock, 0) != hipSuccess)
+            return -1;
+        const uint64_t resident = (uint64_t)(per_cu > 0 ? per_cu : 1) * (uint64_t)device_cus();
+        int lr = 0;
+        while (lr < 4 && (8ull << (lr + 1)) * 2 <= resident) ++lr;
+        return lr + 1;
+    });
+}
+
+// The P onesweep launches of one sort.
+template <int IPT, class UK, class UV, int KIND, bool PAIRS, bool DESC, bool MATCH>
+int rs_passes(const RsBuffers<UK, UV> &buf, uint64_t n, uint64_t tiles, int P, const uint32_t *bins,
+              const LbState &regions, const uint32_t *hot, const uint32_t *plan, const WaitCtl &ctl, hipStream_t s)
+{
+    const int lr1 = rs_log_run<IPT, UK, UV, KIND, PAIRS, DESC, MATCH>();
+    if (lr1 < 0) return LCPP_ERR_HIP;
+    const uint32_t log_run = (uint32_t)(lr1 - 1);
+    for (int p = 0; p < P; ++p) {
+        LCPP_LAUNCH("rs_onesweep", s,
+                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC, MATCH><<<(uint32_t)tiles, kOsBlock, 0, s>>>(
+                        buf, (uint32_t)n, (uint32_t)(p * kRadixBits), bins + p * kRadix, regions, log_run, hot + p,
+                        plan + p, ctl)));
+        LCPP_CHECK_LAUNCH();
+    }
+    return LCPP_OK;
+}
+
 template <class UK, class UV, int KIND, bool PAIRS, bool DESC>
 int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const void *vin_, void *vout_, uint64_t n,
            hipStream_t s)
@@ -794,33 +1013,15 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
                         plan + P, hot, plan));
         LCPP_CHECK_LAUNCH();
     }
-    // XCD run length: 8R <= half the onesweep workgroups resident at once
-    static DeviceCache run_cache;  // log2(R) + 1, or -1 when the occupancy query fails
-    const int lr1 = device_cached(run_cache, [] {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, reinterpret_cast<const void *>(&rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC>),
-                kOsBlock, 0) != hipSuccess)
-            return -1;
-        const uint64_t resident = (uint64_t)(per_cu > 0 ? per_cu : 1) * (uint64_t)device_cus();
-        int lr = 0;
-        while (lr < 4 && (8ull << (lr + 1)) * 2 <= resident) ++lr;
-        return lr + 1;
-    });
-    if (lr1 < 0) return LCPP_ERR_HIP;
-    const uint32_t log_run = (uint32_t)(lr1 - 1);
+    const int path = rs_rank_path(s);
     const WaitCtl ctl = wait_ctl(status);
     // buffers and look-back regions per pass come from the device-side plan
     const RsBuffers<UK, UV> buf{kin, ktmp, kout, vin, vtmp, vout};
     const LbState regions{tc[0], bw[0], tc[1], bw[1]};
-    for (int p = 0; p < P; ++p) {
-        LCPP_LAUNCH("rs_onesweep", s,
-                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
-                        buf, (uint32_t)n, (uint32_t)(p * kRadixBits), bins + p * kRadix, regions, log_run,
-                        hot + p, plan + p, ctl)));
-        LCPP_CHECK_LAUNCH();
-    }
-    return LCPP_OK;
+    return path == kRankMatch
+               ? rs_passes<IPT, UK, UV, KIND, PAIRS, DESC, true>(buf, n, L.tiles, P, bins, regions, hot, plan, ctl, s)
+               : rs_passes<IPT, UK, UV, KIND, PAIRS, DESC, false>(buf, n, L.tiles, P, bins, regions, hot, plan, ctl,
+                                                                  s);
 }
 
 int key_kind(lcpp_dtype k)
@@ -945,4 +1146,18 @@ extern "C" int lcpp_radix_sort_pairs_descending(lcpp_dtype k, lcpp_dtype v, void
                                                 void *vals_out, uint64_t n, void *stream)
 {
     return sort_pairs(k, v, temp, tb, keys_in, keys_out, vals_in, vals_out, n, true, stream);
+}
+
+extern "C" int lcpp_test_set_sort_rank_path(int mode)
+{
+    if (mode < 0 || mode > 2) return LCPP_ERR_INVALID_ARG;
+    g_rank_force.store(mode, std::memory_order_relaxed);
+    return LCPP_OK;
+}
+
+extern "C" int lcpp_radix_sort_rank_path(int *path)
+{
+    if (!path) return LCPP_ERR_INVALID_ARG;
+    *path = rs_rank_path(nullptr);
+    return LCPP_OK;
 }

@@ -138,6 +138,11 @@ def test_unsupported_dtype_and_null_args(L):
     assert L.lcpp_reduce_transform(0, 7, 0, None, 0, None, None, 10, ctypes.byref(one), None) == -1  # bad op
     assert L.lcpp_reduce_transform(0, 0, 9, None, 0, None, None, 10, ctypes.byref(one), None) == -1  # bad transform
     assert L.lcpp_scan_exclusive_sum(0, None, 0, None, None, 10, None) == -1
+    dummy = ctypes.c_void_p(0x1000)
+    assert L.lcpp_scan_exclusive(0, 7, dummy, 1 << 20, dummy, dummy, 10, None, None) == -1  # bad op
+    assert L.lcpp_scan_inclusive(9, 0, dummy, 1 << 20, dummy, dummy, 10, None, None) == -3
+    assert L.lcpp_scan_inclusive(0, 1, None, 0, None, None, 10, None, None) == -1
+    assert L.lcpp_scan_exclusive(0, 2, None, 0, None, None, 0, None, None) == 0  # n = 0: nothing to do
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 10, None) == -1
     assert L.lcpp_radix_sort_keys(1, None, 0, None, None, 1 << 30, None) == -1  # no temp
     dummy = ctypes.c_void_p(0x1000)
@@ -185,6 +190,10 @@ def test_device_status_decode_and_hooks(L):
     assert L.lcpp_status_string(-5) == b"LCPP_ERR_LOOKBACK_TIMEOUT"
     assert L.lcpp_test_set_lookback_fault(3, 16) == 0
     assert L.lcpp_test_set_lookback_fault(0xFFFFFFFF, 0) == 0  # back to the defaults
+    # the sort's rank-path override: 0 (probe), 1 (LDS atomics), 2 (ballot match)
+    assert L.lcpp_test_set_sort_rank_path(3) == -1 and L.lcpp_test_set_sort_rank_path(-1) == -1
+    assert L.lcpp_test_set_sort_rank_path(2) == 0 and L.lcpp_test_set_sort_rank_path(0) == 0
+    assert L.lcpp_radix_sort_rank_path(None) == -1
 
 
 def test_misaligned_temp_rejected(L):
