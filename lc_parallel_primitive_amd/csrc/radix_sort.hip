@@ -22,10 +22,10 @@
 //    once into an LDS table in which every lane of a wave counts into its
 //    own column (16 lane copies of every counter for 8-byte keys), so that
 //    equal digits in one wave (skewed or constant key bytes) never hit one
-//    LDS address; flushed with one global atomic per non-zero bin.  It also zeroes the look-back state of pass 0.  The last
-//    workgroup to finish (the arrival counter, release/acquire at agent
-//    scope) finds each pass's hot digit and plans the passes from the
-//    finished histograms (below).
+//    LDS address; flushed with one global atomic per non-zero bin.  It also
+//    zeroes the look-back state of four passes.  The last workgroup to finish
+//    (the arrival counter, release/acquire at agent scope) finds each pass's
+//    hot digit and plans the passes from the finished histograms (below).
 //  * launches 2..P+1 "rs_onesweep": one 16384-key tile (8192 for 8-byte keys
 //    or values) per 512-thread workgroup.  No ticket: tiles are mapped from
 //    the workgroup id so that every R consecutive tiles (R = 16 on a full
@@ -57,9 +57,11 @@
 //    all 32 bits.  Every wait is on an earlier tile, every re-poll reloads all
 //    the words it still waits on, and a wait that exhausts its bounded spin
 //    records the give-up in the call's status word.  Words are accessed with
-//    agent-scope atomics (the 8 XCD L2s are not coherent).  Two look-back
-//    regions alternate between passes and tiles clear their slots of the
-//    other region for the next pass (no per-pass memset launch).
+//    agent-scope atomics (the 8 XCD L2s are not coherent).  Four look-back
+//    regions, zeroed by the histogram launch, whose write bandwidth is
+//    otherwise idle, serve four passes (no memset launch; only sorts with
+//    more than four data-moving passes re-zero a region inside a pass); tile
+//    counts are 16-bit words.
 //  * The sorted tile leaves through LDS in two halves (32 KB of staging
 //    instead of 64 KB), which lets keys-only passes run three workgroups per
 //    CU: consecutive threads write consecutive positions of each digit run.
@@ -86,8 +88,10 @@ constexpr int kOsWaves = kOsBlock / kWave;
 constexpr int kBatch = 8;      // tiles per look-back batch
 constexpr int kHistBlock = 1024;
 constexpr uint32_t kLbGlobal = 0x80000000u;
-constexpr uint32_t kLbPartial = 0x40000000u;
-constexpr uint32_t kLbMask = 0x3FFFFFFFu;
+// Tile count words are 16-bit: {published:1 | count:15} (a count is at most
+// 16384); 0 = not published yet.
+constexpr uint32_t kTcPublished = 0x8000u;
+constexpr uint32_t kTcMask = 0x7FFFu;
 constexpr uint64_t kMaxItems = 0xFFFFFFFFull;  // 32-bit positions and counts
 
 enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
@@ -164,9 +168,9 @@ __device__ __forceinline__ uint32_t digit_excl_scan(uint32_t x, uint32_t *s_wsum
 // Agent-scope (sc1) loads through a buffer resource: one VGPR offset per
 // load, constant strides folded into the immediate offset (the look-back
 // runs while every key of the tile is held in registers).
-__device__ __forceinline__ uint32_t ld_agent32(__amdgpu_buffer_rsrc_t r, uint32_t off)
+__device__ __forceinline__ uint32_t ld_agent16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kPolicySc1);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kPolicySc1);
 }
 __device__ __forceinline__ uint64_t ld_agent64(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
@@ -209,14 +213,17 @@ __global__ __launch_bounds__(256) void rs_init_kernel(uint32_t *words, uint32_t 
 // plan[p]: a pass whose digit is the same for every key is the identity
 // permutation (the sort is stable), so it is skipped: its launch returns at
 // once.  The other passes ping-pong between the scratch and the output so
-// that the last of them writes the output (the input is never written), and
-// the k-th of them uses look-back region k & 1 (the histogram cleared region
-// 0; each pass clears the other region for the next one).  When every pass
-// is skipped, the last launch copies the input to the output.  SortPairs of
+// that the last of them writes the output (the input is never written).
+// The k-th of them uses look-back region k % 4; the histogram zeroed all four,
+// and when more than four passes move data, pass k >= 1 zeroes region
+// (k - 1) % 4 again for pass k + 3.  When every pass is skipped, the last
+// launch copies the input to the output.  SortPairs of
 // u64 keys with 16 random low bits (6 of 8 passes skipped): 5.21 -> ~1.5 ms.
 // One workgroup; one wave per pass at a time.
 constexpr uint32_t kPlanSkip = 1u, kPlanCopy = 2u;
 constexpr int kPlanSrcShift = 2, kPlanDstShift = 4, kPlanRegionShift = 6;
+constexpr uint32_t kPlanClearPrev = 1u << 8;  // zero region (k - 1) % 4 for pass k + 3
+constexpr int kLbRegions = 4;
 enum PlanBuf : uint32_t { kBufIn = 0, kBufTmp = 1, kBufOut = 2 };
 // Runs in the histogram's last workgroup (NT threads), after the acquire that
 // pairs with every workgroup's release of its bin adds.
@@ -254,7 +261,8 @@ __device__ void rs_make_plan(const uint32_t *bins, uint32_t passes, uint64_t n, 
                 plan[p] = kPlanSkip | (p + 1 == passes && m == 0 ? kPlanCopy : 0u);
             } else {
                 const uint32_t dst = (m - 1 - k) % 2 == 0 ? kBufOut : kBufTmp;  // the last one writes the output
-                plan[p] = (cur << kPlanSrcShift) | (dst << kPlanDstShift) | ((k & 1u) << kPlanRegionShift);
+                plan[p] = (cur << kPlanSrcShift) | (dst << kPlanDstShift) | ((k % kLbRegions) << kPlanRegionShift) |
+                          (k >= 1 && k + kLbRegions - 1 < m ? kPlanClearPrev : 0u);
                 cur = dst;
                 ++k;
             }
@@ -298,9 +306,8 @@ constexpr uint64_t kHistRoundSteps = 255;  // loop steps between flushes of the 
 
 template <class UK, int KIND, bool DESC>
 __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
-    const UK *__restrict__ keys, uint64_t n, uint64_t chunk, uint32_t *bins, uint32_t *__restrict__ clear0,
-    uint64_t clear0_words, uint32_t *__restrict__ clear1, uint64_t clear1_words, uint32_t *arrivals,
-    uint32_t *__restrict__ hot, uint32_t *__restrict__ plan)
+    const UK *__restrict__ keys, uint64_t n, uint64_t chunk, uint32_t *bins, u32x4 *__restrict__ clear,
+    uint64_t clear_vecs, uint32_t *arrivals, uint32_t *__restrict__ hot, uint32_t *__restrict__ plan)
 {
     constexpr int P = sizeof(UK);
     constexpr bool LC = hist_lane_columns<UK>();
@@ -311,12 +318,19 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     const uint32_t lane = lane_id();
     uint32_t *s_last = s_hist + W, *s_trivial = s_last + 1;
     for (uint32_t i = tid; i < W; i += kHistBlock) s_hist[i] = 0;
-    // zero the look-back state of pass 0 (before the counts, so that the
-    // release below covers these stores as well)
-    const uint64_t stride = (uint64_t)gridDim.x * kHistBlock;
-    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear0_words; i += stride) clear0[i] = 0;
-    for (uint64_t i = (uint64_t)blockIdx.x * kHistBlock + tid; i < clear1_words; i += stride) clear1[i] = 0;
     __syncthreads();
+    // The look-back state of four passes is zeroed here, one 16-byte store per
+    // thread per loop step (this workgroup's share of it, front to back), so
+    // the stores go out beside the key stream instead of before it (2^28 u32
+    // keys: 48 MiB of state).  The arrival's release below covers them.
+    const uint64_t cshare = ceil_div(clear_vecs, (uint64_t)gridDim.x);
+    const uint64_t c0 = (uint64_t)blockIdx.x * cshare;
+    const uint64_t c1 = c0 + cshare < clear_vecs ? c0 + cshare : clear_vecs;
+    uint64_t cnext = c0 + tid;
+    auto clear_step = [&]() {
+        if (cnext < c1) __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, clear + cnext);
+        cnext += kHistBlock;
+    };
 
     const uint64_t b0 = (uint64_t)blockIdx.x * chunk;
     const uint64_t b1 = b0 + chunk < n ? b0 + chunk : n;
@@ -370,6 +384,7 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
                 u32x4 v[kVecs];
 #pragma unroll
                 for (int i = 0; i < kVecs; ++i) v[i] = ld16_nt(keys + t + ((uint64_t)i * kHistBlock + tid) * V);
+                clear_step();
 #pragma unroll
                 for (int i = 0; i < kVecs; ++i) {
                     UK e[V];
@@ -384,6 +399,7 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
         r0 = r1;
         if (r0 < b1) flush(true);
     }
+    while (cnext < c1) clear_step();  // what the loop steps did not cover
     flush(false);
 
     // The last workgroup to arrive plans the passes (hot digits, skipped
@@ -430,14 +446,15 @@ constexpr int os_waves_per_eu()
     return PAIRS && (sizeof(UK) == 8 || sizeof(UV) == 8) ? 4 : 6;
 }
 
-// Look-back state of one pass: tcount[tiles][256] (tile digit counts,
-// written once) and bword[batches][256] (batch aggregate and batch inclusive
-// prefix, see batch_word_state).
+// Look-back state: kLbRegions regions, each of tcount[tiles][256] (16-bit
+// tile digit counts, written once) and bword[batches][256] (batch aggregate
+// and batch inclusive prefix, see batch_word_state); the plan names a pass's
+// region.  Regions are zeroed before their pass starts (by the histogram, or
+// by a pass that ran before it), so no pass waits on stale words.
 struct LbState {
-    uint32_t *tcount;       // this pass
-    uint64_t *bword;
-    uint32_t *tcount_next;  // the other region, cleared for the next pass
-    uint64_t *bword_next;
+    uint16_t *tcount;     // region 0; region r starts at tcount + r * tc_stride
+    uint64_t *bword;      // region 0; region r starts at bword + r * bw_stride
+    uint64_t tc_stride, bw_stride;
 };
 // The three key (and value) buffers a pass may read or write, picked by the
 // pass plan.
@@ -510,9 +527,11 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     UK *__restrict__ kout = dst_sel == kBufTmp ? buf.ktmp : buf.kout;
     const UV *__restrict__ vin = src_sel == kBufIn ? buf.vin : src_sel == kBufTmp ? buf.vtmp : buf.vout;
     UV *__restrict__ vout = dst_sel == kBufTmp ? buf.vtmp : buf.vout;
-    const LbState lb = ((plan >> kPlanRegionShift) & 1u)
-                           ? LbState{regions.tcount_next, regions.bword_next, regions.tcount, regions.bword}
-                           : regions;
+    const uint32_t region = (plan >> kPlanRegionShift) & (kLbRegions - 1);
+    const struct {
+        uint16_t *tcount;
+        uint64_t *bword;
+    } lb{regions.tcount + region * regions.tc_stride, regions.bword + region * regions.bw_stride};
     const bool publish = tile != ctl.withhold;  // test hook: a withheld tile never publishes
 
     for (uint32_t i = tid; i < (uint32_t)(kOsWaves * kRadix); i += kOsBlock) (&sm.cnt[0][0])[i] = 0;
@@ -609,15 +628,18 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
         }
         if (d == kRadix - 1) total -= (uint32_t)TILE - valid;  // drop the pads
         if (publish) {
-            st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], total | kLbPartial);
+            st_relaxed(&lb.tcount[(size_t)tile * kRadix + d], (uint16_t)(total | kTcPublished));
             // batch 0's word only ever carries its inclusive prefix
             if (batch > 0)
                 __hip_atomic_fetch_add(&lb.bword[(size_t)batch * kRadix + d], kBwArrive + total, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
         }
         sm.total[d] = total;
-        lb.tcount_next[(size_t)tile * kRadix + d] = 0;
-        if (bpos == 0) lb.bword_next[(size_t)batch * kRadix + d] = 0;
+        if (plan & kPlanClearPrev) {
+            const uint32_t prev = (region + kLbRegions - 1) % kLbRegions;
+            regions.tcount[prev * regions.tc_stride + (size_t)tile * kRadix + d] = 0;
+            if (bpos == 0) regions.bword[prev * regions.bw_stride + (size_t)batch * kRadix + d] = 0;
+        }
     }
     const uint32_t dexcl = digit_excl_scan(owner ? total : 0u, sm.wsum[0]);
     if (owner) {
@@ -646,11 +668,11 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     // so a wait costs one round trip however many words it waits on.
     if (!owner && tid < 2u * kRadix) {
         const uint32_t d2 = tid - kRadix;
-        const __amdgpu_buffer_rsrc_t rt = make_rsrc(lb.tcount + (size_t)(tile - bpos) * kRadix, kBatch * kRadix * 4);
-        const uint32_t o2 = d2 * 4u;
+        const __amdgpu_buffer_rsrc_t rt = make_rsrc(lb.tcount + (size_t)(tile - bpos) * kRadix, kBatch * kRadix * 2);
+        const uint32_t o2 = d2 * 2u;
         uint32_t w7[kBatch - 1];
 #pragma unroll
-        for (int k = 0; k < kBatch - 1; ++k) w7[k] = (uint32_t)k < bpos ? ld_agent32(rt, o2 + k * kRadix * 4) : 1u;
+        for (int k = 0; k < kBatch - 1; ++k) w7[k] = (uint32_t)k < bpos ? ld_agent16(rt, o2 + k * kRadix * 2) : 1u;
         for (uint32_t spins = 0;; ++spins) {
             bool all = true;
 #pragma unroll
@@ -664,12 +686,12 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
             asm volatile("" ::: "memory");  // the reloads below are new reads
 #pragma unroll
             for (int k = 0; k < kBatch - 1; ++k)
-                if (w7[k] == 0) w7[k] = ld_agent32(rt, o2 + k * kRadix * 4);
+                if (w7[k] == 0) w7[k] = ld_agent16(rt, o2 + k * kRadix * 2);
         }
         uint32_t within = 0;
 #pragma unroll
         for (int k = 0; k < kBatch - 1; ++k)
-            if ((uint32_t)k < bpos) within += w7[k] & kLbMask;
+            if ((uint32_t)k < bpos) within += w7[k] & kTcMask;
         sm.within[d2] = within;
     }
     uint32_t bexcl = gbase;
@@ -778,10 +800,12 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
 constexpr int os_ipt(int key_bytes, int val_bytes) { return key_bytes == 8 || val_bytes ? 16 : 32; }
 
 // Temp layout: status header | bins[P][256] | hot[P] | plan[P] | arrivals
-// (zeroed together by rs_init) | tile counts x 2 regions | batch words x 2
-// regions | key scratch | value scratch (pairs only).
+// (zeroed together by rs_init) | tile counts x 4 regions | batch words x 4
+// regions (all zeroed by the histogram launch) | key scratch | value scratch
+// (pairs only).
 struct RsLayout {
-    uint64_t passes, tiles, batches, bins_off, hot_off, tc_off, tc_words, bw_off, bw_words, ktmp_off, vtmp_off, total;
+    uint64_t passes, tiles, batches, bins_off, hot_off, tc_off, tc_region, bw_off, bw_region, ktmp_off, vtmp_off,
+        total;
 };
 
 RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
@@ -794,10 +818,10 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
     L.bins_off = kStatusBytes;
     L.hot_off = L.bins_off + L.passes * kRadix * 4;  // hot digits, then the pass plan: one word each per pass
     L.tc_off = align_up(L.hot_off + (2 * L.passes + 1) * 4, 256);  // + the histogram's arrival counter
-    L.tc_words = L.tiles * kRadix;
-    L.bw_off = L.tc_off + align_up(2 * L.tc_words * 4, 256);
-    L.bw_words = L.batches * kRadix;
-    L.ktmp_off = L.bw_off + align_up(2 * L.bw_words * 8, 256);  // 64-bit words
+    L.tc_region = align_up(L.tiles * kRadix * 2, 256);  // 16-bit tile counts
+    L.bw_off = L.tc_off + kLbRegions * L.tc_region;
+    L.bw_region = align_up(L.batches * kRadix * 8, 256);  // 64-bit batch words
+    L.ktmp_off = L.bw_off + kLbRegions * L.bw_region;
     L.vtmp_off = L.ktmp_off + align_up(n * key_bytes, 256);
     L.total = n ? L.vtmp_off + align_up(n * val_bytes, 256) : 0;
     return L;
@@ -942,16 +966,18 @@ int rs_log_run()
 
 // The P onesweep launches of one sort.
 template <int IPT, class UK, class UV, int KIND, bool PAIRS, bool DESC, bool MATCH>
-int rs_passes(const RsBuffers<UK, UV> &buf, uint64_t n, uint64_t tiles, int P, const uint32_t *bins,
-              const LbState &regions, const uint32_t *hot, const uint32_t *plan, const WaitCtl &ctl, hipStream_t s)
+int rs_passes(const RsBuffers<UK, UV> &buf, uint64_t n, const RsLayout &L, char *t, const uint32_t *bins,
+              const uint32_t *hot, const uint32_t *plan, const WaitCtl &ctl, hipStream_t s)
 {
     const int lr1 = rs_log_run<IPT, UK, UV, KIND, PAIRS, DESC, MATCH>();
     if (lr1 < 0) return LCPP_ERR_HIP;
     const uint32_t log_run = (uint32_t)(lr1 - 1);
-    for (int p = 0; p < P; ++p) {
+    for (int p = 0; p < (int)L.passes; ++p) {
+        const LbState lb{reinterpret_cast<uint16_t *>(t + L.tc_off), reinterpret_cast<uint64_t *>(t + L.bw_off),
+                         L.tc_region / 2, L.bw_region / 8};
         LCPP_LAUNCH("rs_onesweep", s,
-                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC, MATCH><<<(uint32_t)tiles, kOsBlock, 0, s>>>(
-                        buf, (uint32_t)n, (uint32_t)(p * kRadixBits), bins + p * kRadix, regions, log_run, hot + p,
+                    (rs_onesweep_kernel<IPT, UK, UV, KIND, PAIRS, DESC, MATCH><<<(uint32_t)L.tiles, kOsBlock, 0, s>>>(
+                        buf, (uint32_t)n, (uint32_t)(p * kRadixBits), bins + p * kRadix, lb, log_run, hot + p,
                         plan + p, ctl)));
         LCPP_CHECK_LAUNCH();
     }
@@ -978,10 +1004,6 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
     uint32_t *bins = reinterpret_cast<uint32_t *>(t + L.bins_off);
     uint32_t *hot = reinterpret_cast<uint32_t *>(t + L.hot_off);
     uint32_t *plan = hot + L.passes;
-    uint32_t *tc[2] = {reinterpret_cast<uint32_t *>(t + L.tc_off),
-                       reinterpret_cast<uint32_t *>(t + L.tc_off) + L.tc_words};
-    uint64_t *bw[2] = {reinterpret_cast<uint64_t *>(t + L.bw_off),
-                       reinterpret_cast<uint64_t *>(t + L.bw_off) + L.bw_words};
     UK *ktmp = reinterpret_cast<UK *>(t + L.ktmp_off);
     UV *vtmp = reinterpret_cast<UV *>(t + L.vtmp_off);
     const int P = (int)L.passes;
@@ -1009,19 +1031,16 @@ int rs_run(void *temp, size_t temp_bytes, const void *kin_, void *kout_, const v
         grid = ceil_div(n, chunk);
         LCPP_LAUNCH("rs_histogram", s,
                     rs_histogram_kernel<UK, KIND, DESC><<<(uint32_t)grid, kHistBlock, lds, s>>>(
-                        kin, n, chunk, bins, tc[0], L.tc_words, reinterpret_cast<uint32_t *>(bw[0]), 2 * L.bw_words,
-                        plan + P, hot, plan));
+                        kin, n, chunk, bins, reinterpret_cast<u32x4 *>(t + L.tc_off),
+                        (L.ktmp_off - L.tc_off) / 16, plan + P, hot, plan));
         LCPP_CHECK_LAUNCH();
     }
     const int path = rs_rank_path(s);
     const WaitCtl ctl = wait_ctl(status);
-    // buffers and look-back regions per pass come from the device-side plan
+    // buffers per pass come from the device-side plan
     const RsBuffers<UK, UV> buf{kin, ktmp, kout, vin, vtmp, vout};
-    const LbState regions{tc[0], bw[0], tc[1], bw[1]};
-    return path == kRankMatch
-               ? rs_passes<IPT, UK, UV, KIND, PAIRS, DESC, true>(buf, n, L.tiles, P, bins, regions, hot, plan, ctl, s)
-               : rs_passes<IPT, UK, UV, KIND, PAIRS, DESC, false>(buf, n, L.tiles, P, bins, regions, hot, plan, ctl,
-                                                                  s);
+    return path == kRankMatch ? rs_passes<IPT, UK, UV, KIND, PAIRS, DESC, true>(buf, n, L, t, bins, hot, plan, ctl, s)
+                              : rs_passes<IPT, UK, UV, KIND, PAIRS, DESC, false>(buf, n, L, t, bins, hot, plan, ctl, s);
 }
 
 int key_kind(lcpp_dtype k)

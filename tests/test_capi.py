@@ -84,17 +84,17 @@ def test_temp_bytes_queries(L):
     rc, b = _q(L.lcpp_scan_temp_bytes, 4, 1 << 27)
     assert rc == 0 and b == HDR + (1 << 14) * 16
     assert _q(L.lcpp_scan_temp_bytes, 1, 0) == (0, 0)
-    # sort: header + bins + hot digits + plan + arrival counter, then 2 regions of
-    # tile counts + 2 regions of 64-bit batch words + key scratch (no value
+    # sort: header + bins + hot digits + plan + arrival counter, then 4 regions
+    # of 16-bit tile counts and 4 of 64-bit batch words + key scratch (no value
     # scratch for keys-only); 16384-key tiles (8192 with values), batches of 8
     rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, 1 << 28)
     tiles = (1 << 28) // 16384
     head = (HDR + 4 * 256 * 4 + (2 * 4 + 1) * 4 + 255) // 256 * 256
-    assert rc == 0 and b == head + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 8 + (1 << 28) * 4
+    assert rc == 0 and b == head + 4 * tiles * 256 * 2 + 4 * (tiles // 8) * 256 * 8 + (1 << 28) * 4
     rc, bp = _q(L.lcpp_radix_sort_pairs_temp_bytes, 4, 1, 1 << 27)
     tiles = (1 << 27) // 8192
     head = (HDR + 8 * 256 * 4 + (2 * 8 + 1) * 4 + 255) // 256 * 256
-    assert rc == 0 and bp == head + 2 * tiles * 256 * 4 + 2 * (tiles // 8) * 256 * 8 + (1 << 27) * 12
+    assert rc == 0 and bp == head + 4 * tiles * 256 * 2 + 4 * (tiles // 8) * 256 * 8 + (1 << 27) * 12
     # the sort takes n up to 2^32 - 1 (32-bit look-back counts and positions)
     rc, b = _q(L.lcpp_radix_sort_keys_temp_bytes, 1, (1 << 32) - 1)
     assert rc == 0 and b > ((1 << 32) - 1) * 4
