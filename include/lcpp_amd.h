@@ -268,7 +268,7 @@ int lcpp_radix_sort_pairs_descending(lcpp_dtype k, lcpp_dtype v, void *temp, siz
  * returning LDS atomics, which are stable only if the LDS serves the lanes of one instruction
  * that hit one address in lane order (gfx950 does; no ISA document promises it), or with a
  * ballot match, stable by construction.  The first sort on each device runs an in-bounds
- * probe of that lane order (~10 us, synchronizes a private stream) and takes the atomic path
+ * probe of that lane order (~70 us, synchronizes a private stream) and takes the atomic path
  * only if the probe sees no violation.  A first sort made while its stream is being captured
  * into a graph takes the match path.  Writes the path the sorts on the current device use:
  * 1 = LDS atomics, 2 = ballot match (running the probe if it has not run on this device). */

@@ -831,7 +831,7 @@ RsLayout rs_layout(uint64_t n, int key_bytes, int val_bytes)
 // The atomic ranking path gives stable ranks only if the LDS serves the lanes
 // of one returning atomic that hit one address in lane order.  That is how
 // gfx950 behaves, but no ISA document promises it, so the first sort on each
-// device runs a probe (~10 us, in bounds): 1024 waves x 32 instructions of
+// device runs a probe (~70 us, in bounds): 1024 waves x 32 instructions of
 // same-address LDS atomics over uniform, hot, constant and two-value digits
 // with varying addends, every result checked against the lane-order value.
 // Any violation selects the match path, which is stable by construction.
