@@ -106,6 +106,13 @@ const char *lcpp_status_string(int status);
  * temp == NULL or temp_bytes < 256: synchronizes and returns LCPP_OK.  This is
  * the one function here that synchronizes (a debug / validation path). */
 int lcpp_temp_status(const void *temp, size_t temp_bytes, void *stream);
+/* The same check without synchronizing: enqueues on `stream` a one-thread kernel that ORs the
+ * status word of the last call that used `temp` into *dst (device memory, or pinned host memory
+ * the device can write).  A caller can accumulate the words of many calls into one and decode it
+ * with lcpp_device_status_decode at its own synchronization point.  Returns LCPP_OK without a
+ * launch when temp == NULL or temp_bytes < 256 (calls whose temp query is 0 keep no status word).
+ * No counterpart in the reference (whose debug check synchronizes). */
+int lcpp_temp_status_record(const void *temp, size_t temp_bytes, uint32_t *dst, void *stream);
 /* The lcpp_status a device status word stands for (pure host arithmetic). */
 int lcpp_device_status_decode(uint32_t word);
 /* hipStreamSynchronize(stream): LCPP_OK or LCPP_ERR_HIP. */

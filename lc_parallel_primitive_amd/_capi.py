@@ -67,6 +67,7 @@ SIGNATURES = {
     "lcpp_segment_reduce_argmin_fixed": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, ctypes.c_uint32, _vp]),
     "lcpp_segment_reduce_argmax_fixed": (_i, [_i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _u64, ctypes.c_uint32, _vp]),
     "lcpp_temp_status": (_i, [_vp, ctypes.c_size_t, _vp]),
+    "lcpp_temp_status_record": (_i, [_vp, ctypes.c_size_t, _vp, _vp]),
     "lcpp_device_status_decode": (_i, [ctypes.c_uint32]),
     "lcpp_stream_sync": (_i, [_vp]),
     "lcpp_test_set_lookback_fault": (_i, [ctypes.c_uint32, ctypes.c_uint32]),

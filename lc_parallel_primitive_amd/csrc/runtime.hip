@@ -116,6 +116,25 @@ extern "C" int lcpp_temp_status(const void *temp, size_t temp_bytes, void *strea
     return lcpp_device_status_decode(word);
 }
 
+namespace {
+// dst |= the status word of the call that last used the temp buffer
+__global__ void status_record_kernel(const uint32_t *status, uint32_t *dst)
+{
+    const uint32_t w = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (w) __hip_atomic_fetch_or(dst, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+}  // namespace
+
+extern "C" int lcpp_temp_status_record(const void *temp, size_t temp_bytes, uint32_t *dst, void *stream)
+{
+    if (!dst) return LCPP_ERR_INVALID_ARG;
+    if (!temp || temp_bytes < kStatusBytes) return LCPP_OK;  // that call keeps no status word
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    LCPP_LAUNCH("status_record", s,
+                status_record_kernel<<<1, 1, 0, s>>>(static_cast<const uint32_t *>(temp), dst));
+    return hipGetLastError() == hipSuccess ? LCPP_OK : LCPP_ERR_HIP;
+}
+
 extern "C" int lcpp_test_set_lookback_fault(uint32_t withhold_tile, uint32_t spin_limit)
 {
     g_withhold.store(withhold_tile, std::memory_order_relaxed);

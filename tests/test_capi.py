@@ -194,6 +194,10 @@ def test_device_status_decode_and_hooks(L):
     assert L.lcpp_test_set_sort_rank_path(3) == -1 and L.lcpp_test_set_sort_rank_path(-1) == -1
     assert L.lcpp_test_set_sort_rank_path(2) == 0 and L.lcpp_test_set_sort_rank_path(0) == 0
     assert L.lcpp_radix_sort_rank_path(None) == -1
+    assert L.lcpp_temp_status_record(None, 0, None, None) == -1  # no destination
+    dummy = ctypes.c_void_p(0x1000)
+    assert L.lcpp_temp_status_record(None, 0, dummy, None) == 0  # no temp: nothing to record, no launch
+    assert L.lcpp_temp_status_record(dummy, 255, dummy, None) == 0
 
 
 def test_misaligned_temp_rejected(L):

@@ -107,6 +107,40 @@ def test_sort_withheld_tile_reports_timeout(gpu, pairs):
         assert (g.to_host(ko) == o.radix_sort(k)).all()
 
 
+def test_status_record_accumulates_without_synchronizing(gpu):
+    """lcpp_temp_status_record ORs each call's status word into a caller word
+    on the stream: three sorts (normal, one with a withheld tile, normal again)
+    leave the bit set in the accumulated word, a clean word stays 0, and
+    a call without temp storage records nothing."""
+    import torch
+
+    import gpu_util as g
+
+    L = _L()
+    n = 20 * 16384 + 3
+    k = g.random_array(np.uint32, n, seed=5)
+    dk, ko = g.to_dev(k), g.empty(n, np.uint32)
+    t = _temp(L.lcpp_radix_sort_keys_temp_bytes, 1, n)
+    acc = torch.zeros(1, dtype=torch.int32, device="cuda")
+    clean = torch.zeros(1, dtype=torch.int32, device="cuda")
+    log("status record: three sorts, the second with tile 7 withheld")
+    assert L.lcpp_radix_sort_keys(1, _p(t), t.numel(), _p(dk), _p(ko), n, _sp()) == 0
+    assert L.lcpp_temp_status_record(_p(t), t.numel(), _p(acc), _sp()) == 0
+    assert L.lcpp_temp_status_record(_p(t), t.numel(), _p(clean), _sp()) == 0
+    with withheld(7):
+        assert L.lcpp_radix_sort_keys(1, _p(t), t.numel(), _p(dk), _p(ko), n, _sp()) == 0
+        assert L.lcpp_temp_status_record(_p(t), t.numel(), _p(acc), _sp()) == 0
+    assert L.lcpp_radix_sort_keys(1, _p(t), t.numel(), _p(dk), _p(ko), n, _sp()) == 0
+    assert L.lcpp_temp_status_record(_p(t), t.numel(), _p(acc), _sp()) == 0
+    assert L.lcpp_temp_status_record(None, 0, _p(acc), _sp()) == 0  # no temp: nothing recorded
+    assert L.lcpp_temp_status_record(_p(t), t.numel(), None, _sp()) == -1
+    torch.cuda.synchronize()
+    word = int(acc.item()) & 0xFFFFFFFF
+    assert word & 1 and L.lcpp_device_status_decode(word) == TIMEOUT
+    assert int(clean.item()) == 0
+    assert (g.to_host(ko) == o.radix_sort(k)).all()  # the last call was a normal one
+
+
 def test_by_key_withheld_tile_reports_timeout(gpu):
     import gpu_util as g
 
