@@ -209,6 +209,17 @@ class DeviceReduce : public LuisaModule {
                                  d_out.data(), d_index_out.data(), num_item, cmdlist.stream),
               "DeviceReduce::ArgMax", cmdlist.stream, temp_storage);
     }
+    /* device/device_reduce.h:131-147 (reduce_op: SumOp, MinOp or MaxOp):
+     * d_out[0] = reduce_op(initial_value, reduce_op over d_in[0..num_item)) */
+    template <class T, class ReduceOp>
+    void Reduce(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                size_t num_item, ReduceOp, T initial_value)
+    {
+        check(lcpp_reduce_transform(dtype_of<T>(), reduce_op_of<ReduceOp>(), LCPP_XFORM_IDENTITY,
+                                    temp_storage.data(), temp_storage.size_bytes(), d_in.data(), d_out.data(),
+                                    num_item, &initial_value, cmdlist.stream),
+              "DeviceReduce::Reduce", cmdlist.stream, temp_storage);
+    }
     /* device/device_reduce.h:331-348 */
     template <class T, class ReduceOp, class TransformOp>
     void TransformReduce(CommandList &cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,

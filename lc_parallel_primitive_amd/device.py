@@ -139,6 +139,11 @@ class DeviceReduce(_Module):
         """device_reduce.h:229-272: largest value, ties to the largest index (ArgMaxOp)."""
         self._arg(lib().lcpp_reduce_argmax, temp_storage, d_in, d_out, d_index_out, num_item, stream)
 
+    def Reduce(self, temp_storage, d_in, d_out, num_item: int, reduce_op: str, initial_value, stream=None):
+        """device_reduce.h:131-147: d_out[0] = reduce_op(initial_value, reduce_op over d_in[0..num_item)).
+        reduce_op: "sum" | "min" | "max"."""
+        self.TransformReduce(temp_storage, d_in, d_out, num_item, reduce_op, "identity", initial_value, stream)
+
     def TransformReduce(self, temp_storage, d_in, d_out, num_item: int, reduce_op: str, transform_op: str, init,
                         stream=None):
         """device_reduce.h:331-348: d_out[0] = reduce_op(init, reduce_op over i of transform_op(d_in[i])).

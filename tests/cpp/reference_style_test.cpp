@@ -117,6 +117,12 @@ void test_reduce()
     expect(out.download(1)[0] == *std::max_element(a.begin(), a.end()), "DeviceReduce::Max shuffled");
     reducer.Sum(cmdlist, temp.view(), in.view(), out.view(), a.size());
     expect(out.download(1)[0] == std::accumulate(a.begin(), a.end(), 0), "DeviceReduce::Sum shuffled");
+    reducer.Reduce(cmdlist, temp.view(), in.view(), out.view(), a.size(), SumOp{}, 1000);
+    expect(out.download(1)[0] == std::accumulate(a.begin(), a.end(), 1000), "DeviceReduce::Reduce SumOp init 1000");
+    reducer.Reduce(cmdlist, temp.view(), in.view(), out.view(), a.size(), MinOp{}, -7);
+    expect(out.download(1)[0] == -7, "DeviceReduce::Reduce MinOp init below every element");
+    reducer.Reduce(cmdlist, temp.view(), in.view(), out.view(), a.size(), MaxOp{}, 100);
+    expect(out.download(1)[0] == *std::max_element(a.begin(), a.end()), "DeviceReduce::Reduce MaxOp");
     reducer.ArgMax(cmdlist, temp.view(), in.view(), out.view(), idx.view(), a.size());
     expect(idx.download(1)[0] == uint(std::max_element(a.begin(), a.end()) - a.begin()), "DeviceReduce::ArgMax shuffled");
     reducer.ArgMin(cmdlist, temp.view(), in.view(), out.view(), idx.view(), a.size());

@@ -227,6 +227,30 @@ def test_transform_vs_oracle(gpu, dtype, op, xf):
         assert got == o.reduce_transform(OPS[op], XFS[xf], a, init)
 
 
+@pytest.mark.parametrize("dtype", [np.int32, np.uint64, np.float64])
+@pytest.mark.parametrize("op", list(OPS))
+def test_reduce_with_initial_value(gpu, dtype, op):
+    """DeviceReduce::Reduce(reduce_op, initial_value) (device_reduce.h:131-147):
+    the oracle's fold from init (integers exact), floats against float64."""
+    import gpu_util as g
+    from lc_parallel_primitive_amd import DeviceReduce
+
+    n = 100_003
+    a = g.random_array(dtype, n, seed=23)
+    d = g.to_dev(a)
+    out = g.empty(1, dtype)
+    init = np.array([-5 if np.dtype(dtype).kind != "u" else 5], dtype=dtype)[0]
+    tmp = g.temp(DeviceReduce.GetTempStorageBytes(np.dtype(dtype).name, n))
+    DeviceReduce().Reduce(tmp, d, out, n, op, init)
+    got = g.to_host(out)[0]
+    if np.dtype(dtype).kind == "f" and op == "sum":
+        t = a.astype(np.float64)
+        s, ab = float(t.sum()) + float(init), float(np.abs(t).sum()) + abs(float(init))
+        assert abs(float(got) - s) <= RTOL_SUM * ab
+    else:
+        assert got == o.reduce_transform(OPS[op], o.XF_IDENTITY, a, init)
+
+
 def test_past_2p32_elements(gpu):
     """Sum of n = 2^32 + 12345 int32 ones wraps to 12345; ArgMax/ArgMin over
     n = 2^32 - 1 elements (the most that 32-bit indices allow): ties of ones
