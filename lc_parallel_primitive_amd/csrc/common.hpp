@@ -24,6 +24,17 @@ __device__ __forceinline__ uint32_t lane_id()
     return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
 }
 
+// Orders one wave's LDS accesses around a hand-off between its lanes (a
+// lane reads what another lane of the same wave wrote): the LDS serves a
+// wave's instructions in issue order, so only the compiler must not move
+// accesses across this point.
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // popcount(mask & lanes_below_me): rank of this lane among the lanes of `mask`.
 __device__ __forceinline__ uint32_t mask_rank(uint64_t mask)
 {

@@ -81,6 +81,15 @@ RbkLayout<K, V> rbk_layout(uint64_t n)
 
 __global__ void rbk_zero_runs(uint32_t *num_runs) { *num_runs = 0; }
 
+// The bits of `f` as a To of the same size (pass 2 stages values in the key
+// array only when the sizes match; other instantiations never call it).
+template <class To, class From>
+__device__ __forceinline__ To same_size_bits(From f)
+{
+    if constexpr (sizeof(To) == sizeof(From)) return __builtin_bit_cast(To, f);
+    else return To{};
+}
+
 // LDS of one tile.  Keys sit in LDS when they fit in 32 KiB: the registers
 // that held them are free for pass 2 (150 -> ~100 VGPRs).
 template <class K, class V>
@@ -235,42 +244,136 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
     const uint32_t cpre = direct ? s_cpre : 0u;
     const V vpre = direct ? s_vpre : ident;
 
-    // pass 2: rescan from the slice prefixes; a head closes the run before it
-    const uint32_t pf = sm.pf;
+    // pass 2: rescan from the slice prefixes; a head closes the run before it.
+    // STAGE (a direct tile with more runs than half its elements, keys in
+    // LDS, keys and values of one size): each (vector, wave) slice's runs go
+    // out through that slice's own part of sm.keys once its keys are read,
+    // so that consecutive lanes store consecutive runs.  A slice with at most
+    // half as many runs as elements puts keys and values there side by side
+    // and is stored after the last vector (one wait for all of them); a
+    // denser one goes out at once, keys then values.  Other direct tiles
+    // store each run where it closes.
+    constexpr bool kStageDirect = kKeysInLds && sizeof(K) == sizeof(V);
+    auto pass2 = [&](auto stage_tag) {
+        constexpr bool STAGE = decltype(stage_tag)::value;
+        constexpr uint32_t kSliceHalf = kWave * VP / 2;
+        uint32_t deferred = 0;  // STAGE, bit k: slice (k, wave) waits in LDS for the final stores
+        const uint32_t pf = sm.pf;
 #pragma unroll
-    for (int k = 0; k < kBkVecs; ++k) {
-        const uint32_t sl = k * kBkWaves + wave;
-        const V pw0 = sm.pw[sl];
-        const V pw = ((pf >> sl) & 1u) ? pw0 : op(vpre, pw0);
-        V s = ((exF >> k) & 1u) ? exS[k] : op(pw, exS[k]);
-        // staged: the tile's heads before this item (its entry index);
-        // direct: all heads before it (it closes run c - 1)
-        uint32_t c = cpre + sm.cw[sl] + exC[k];
+        for (int k = 0; k < kBkVecs; ++k) {
+            const uint32_t sl = k * kBkWaves + wave;
+            const V pw0 = sm.pw[sl];
+            const V pw = ((pf >> sl) & 1u) ? pw0 : op(vpre, pw0);
+            V s = ((exF >> k) & 1u) ? exS[k] : op(pw, exS[k]);
+            // staged: the tile's heads before this item (its entry index);
+            // direct: all heads before it (it closes run c - 1)
+            uint32_t c = cpre + sm.cw[sl] + exC[k];
+            K ek[VP];  // STAGE: this thread's runs, in order
+            V ev[VP];
 #pragma unroll
-        for (int j = 0; j < VP; ++j) {
-            const uint32_t e = bk_elem<V>(k, tid, j);
-            if ((fl >> (k * VP + j)) & 1u) {
-                K key;
-                if constexpr (kKeysInLds) key = e > 0 ? sm.keys[e - 1] : sm.pred;
-                else key = j > 0 ? r.key[k][j - 1] : prev0[k];
-                if (direct) {
-                    // c - 1 < n by construction; the bound keeps a broken
-                    // invariant (a wait past its spin limit) from writing
-                    // outside the outputs
-                    if (c > 0 && c - 1 < n) {
-                        unique_out[c - 1] = key;
-                        agg_out[c - 1] = s;
+            for (int j = 0; j < VP; ++j) {
+                const uint32_t e = bk_elem<V>(k, tid, j);
+                if ((fl >> (k * VP + j)) & 1u) {
+                    K key;
+                    if constexpr (STAGE) {
+                        // a slice's key before it is the previous slice's
+                        // last key (its part of sm.keys may be rewritten)
+                        if (j == 0 && lane == 0)
+                            key = wave > 0 ? sm.last[k][wave - 1] : k > 0 ? sm.last[k - 1][kBkWaves - 1] : sm.pred;
+                        else
+                            key = sm.keys[e - 1];
+                        ek[j] = key;
+                        ev[j] = s;
+                    } else {
+                        if constexpr (kKeysInLds) key = e > 0 ? sm.keys[e - 1] : sm.pred;
+                        else key = j > 0 ? r.key[k][j - 1] : prev0[k];
+                        if (direct) {
+                            // c - 1 < n by construction; the bound keeps a
+                            // broken invariant (a wait past its spin limit)
+                            // from writing outside the outputs
+                            if (c > 0 && c - 1 < n) {
+                                unique_out[c - 1] = key;
+                                agg_out[c - 1] = s;
+                            }
+                        } else {
+                            sm.stk[c] = key;  // c < the tile's head count <= kRbkSlot
+                            sm.stv[c] = s;
+                        }
+                        ++c;
                     }
+                    s = r.val[k][j];
                 } else {
-                    sm.stk[c] = key;  // c < the tile's head count <= kRbkSlot
-                    sm.stv[c] = s;
+                    s = op(s, r.val[k][j]);  // identity past n
                 }
-                ++c;
-                s = r.val[k][j];
-            } else {
-                s = op(s, r.val[k][j]);  // identity past n
+            }
+            if constexpr (STAGE) {
+                // the slice: elements [ss, ss + 64 VP), runs [cb, cb + nsl)
+                // of the count (run i closes at output position cb + i - 1)
+                const uint32_t ss = bk_elem<V>(k, wave * kWave, 0);
+                const uint32_t cb = cpre + sm.cw[sl], nsl = sm.C[k][wave];
+                wave_lds_sync();  // every lane has read its keys of the slice
+                uint32_t li = exC[k];
+                if (nsl <= kSliceHalf) {
+#pragma unroll
+                    for (int j = 0; j < VP; ++j)
+                        if ((fl >> (k * VP + j)) & 1u) {
+                            sm.keys[ss + li] = ek[j];
+                            sm.keys[ss + kSliceHalf + li] = same_size_bits<K>(ev[j]);
+                            ++li;
+                        }
+                    deferred |= 1u << k;
+                    continue;
+                }
+#pragma unroll
+                for (int j = 0; j < VP; ++j)
+                    if ((fl >> (k * VP + j)) & 1u) sm.keys[ss + li++] = ek[j];
+                wave_lds_sync();
+#pragma unroll
+                for (int q = 0; q < VP; ++q) {
+                    const uint32_t i = q * kWave + lane;
+                    // the bound keeps a broken invariant (a wait past its
+                    // spin limit) from writing outside the outputs
+                    if (i < nsl && cb + i > 0 && cb + i - 1 < n) unique_out[cb + i - 1] = sm.keys[ss + i];
+                }
+                wave_lds_sync();
+                li = exC[k];
+#pragma unroll
+                for (int j = 0; j < VP; ++j)
+                    if ((fl >> (k * VP + j)) & 1u) sm.keys[ss + li++] = same_size_bits<K>(ev[j]);
+                wave_lds_sync();
+#pragma unroll
+                for (int q = 0; q < VP; ++q) {
+                    const uint32_t i = q * kWave + lane;
+                    if (i < nsl && cb + i > 0 && cb + i - 1 < n)
+                        agg_out[cb + i - 1] = same_size_bits<V>(sm.keys[ss + i]);
+                }
             }
         }
+        if constexpr (STAGE) {
+            if (deferred) {
+                wave_lds_sync();
+#pragma unroll
+                for (int k = 0; k < kBkVecs; ++k) {
+                    if (!((deferred >> k) & 1u)) continue;
+                    const uint32_t ss = bk_elem<V>(k, wave * kWave, 0);
+                    const uint32_t cb = cpre + sm.cw[k * kBkWaves + wave], nsl = sm.C[k][wave];
+#pragma unroll
+                    for (uint32_t q = 0; q < kSliceHalf / kWave; ++q) {
+                        const uint32_t i = q * kWave + lane;
+                        if (i < nsl && cb + i > 0 && cb + i - 1 < n) {
+                            unique_out[cb + i - 1] = sm.keys[ss + i];
+                            agg_out[cb + i - 1] = same_size_bits<V>(sm.keys[ss + kSliceHalf + i]);
+                        }
+                    }
+                }
+            }
+        }
+    };
+    if constexpr (kStageDirect) {
+        if (direct && sm.tc > TILE / 2) pass2(std::true_type{});
+        else pass2(std::false_type{});
+    } else {
+        pass2(std::false_type{});
     }
     if (!direct) {
         __syncthreads();

@@ -259,6 +259,36 @@ def test_reduce_by_key_dense_and_sparse_tiles_mixed(gpu, op):
     assert (uk[r:] == 0).all() and (ag[r:] == 0).all()
 
 
+@pytest.mark.parametrize("kdt,vdt", [(np.int32, np.int32), (np.uint32, np.float32), (np.float32, np.int32),
+                                     (np.int64, np.int64), (np.float64, np.float64), (np.uint64, np.float64),
+                                     (np.int32, np.int64), (np.int64, np.int32)])
+@pytest.mark.parametrize("op", ["sum", "min", "max"])
+def test_reduce_by_key_direct_tile_densities(gpu, kdt, vdt, op):
+    """Tiles with more than 128 runs write them out themselves.  When more
+    than half of a tile's elements start a run (and keys and values have one
+    size) the runs go out through each wave slice's part of the tile's keys
+    in LDS: slices with at most half as many runs as elements together at the
+    end of the tile, denser ones at once.  Densities on both sides of both
+    boundaries, every key distinct, a ragged last tile, the first tile (whose
+    first head closes no run), and a guard past the outputs."""
+    tile = 8192 if np.dtype(vdt).itemsize == 4 else 4096
+    n = 5 * tile + 333
+    for mean in (1.0, 1.6, 1.95, 2.0, 2.05, 2.5, 4.0, 16.0, 60.0):
+        keys = np.arange(n).astype(kdt) if mean == 1.0 else run_keys(n, mean, int(mean * 100), kdt)
+        v = values(vdt, n, 21)
+        log(f"ReduceByKey direct tiles {np.dtype(kdt).name}/{np.dtype(vdt).name} mean={mean} {op}")
+        uk, ag, r = reduce_by_key(keys, v, op, guard=8)
+        ek, ea = o.reduce_by_key(keys, v, OPS[op])
+        assert r == ek.size
+        assert uk[:r].tobytes() == ek.tobytes()
+        if np.dtype(vdt).kind == "f" and op == "sum":
+            s_, ab = o.reduce_by_key_f64(keys, v)
+            assert (np.abs(ag[:r].astype(np.float64) - s_) <= RTOL * ab + 1e-30).all()
+        else:
+            assert ag[:r].tobytes() == ea.tobytes()
+        assert (uk[r:] == 0).all() and (ag[r:] == 0).all(), "write past the last run"
+
+
 @pytest.mark.parametrize("n_staged_tiles", [15, 16, 17, 600, 3000])
 def test_reduce_by_key_long_staged_prefix_then_dense(gpu, n_staged_tiles):
     """A long stretch of tiles that stage their runs (they publish only
