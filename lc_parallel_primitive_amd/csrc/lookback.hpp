@@ -128,69 +128,6 @@ __device__ T lb_wait_prefix(const uint64_t *words, uint32_t tile, Op op, T ident
     return excl;
 }
 
-// Look-back for walks that may pass long runs of PARTIAL words (4-byte
-// payloads; ReduceByKey's staged tiles only ever publish PARTIAL counts, so a
-// tile after a long staged stretch would otherwise walk it 16 words per round
-// trip).  The first round trip polls kLbPollWidth predecessors, as
-// lb_wait_prefix does, so a walk that ends there costs the same; when no
-// INCLUSIVE word is among them, every later round trip polls NW windows of 64
-// (all loads issued before any wait): P predecessors take about P / (64 NW)
-// round trips.  Every lane returns the exclusive prefix; a word still
-// unpublished after the spin limit is counted as identity and reported.
-template <int NW, class T, class Op>
-__device__ T lb_wait_prefix_wide(const uint64_t *words, uint32_t tile, Op op, T identity, const WaitCtl &ctl)
-{
-    static_assert(sizeof(T) == 4, "4-byte payloads (one word per tile)");
-    const uint32_t lane = lane_id();
-    T excl = identity;
-    int64_t top = (int64_t)tile - 1;
-    uint32_t spins = 0;
-    bool first = true;
-    for (;;) {
-        uint32_t s[NW];
-        T v[NW];
-#pragma unroll
-        for (int k = 0; k < NW; ++k) {
-            const bool poller = first ? (k == 0 && lane < (uint32_t)kLbPollWidth) : true;
-            const int64_t j = top - (int64_t)k * kWave - (int64_t)lane;
-            const uint64_t w = poller && j >= 0 ? ld_relaxed(&words[j]) : 0ull;
-            s[k] = !poller ? kStPartial : j < 0 ? kStInclusive : (uint32_t)w;
-            v[k] = poller && j >= 0 && s[k] != kStInvalid ? lb_from_bits<T>(w >> 32) : identity;
-        }
-        // the nearest INCLUSIVE word: window k0, lane l0 (k0 = NW: none)
-        int k0 = NW;
-        uint32_t l0 = kWave;
-#pragma unroll
-        for (int k = NW - 1; k >= 0; --k) {
-            const uint64_t m = ballot(s[k] == kStInclusive);
-            if (m) {
-                k0 = k;
-                l0 = (uint32_t)__builtin_ctzll(m);
-            }
-        }
-        bool late = false;
-        T acc = identity;
-#pragma unroll
-        for (int k = 0; k < NW; ++k) {
-            const bool in_range = k < k0 || (k == k0 && lane <= l0);
-            late |= in_range && s[k] == kStInvalid;
-            acc = in_range ? op(acc, v[k]) : acc;
-        }
-        if (ballot(late) != 0) {
-            if (++spins < ctl.spin_limit) {
-                __builtin_amdgcn_s_sleep(1);
-                continue;  // re-poll the same windows
-            }
-            if (lane == 0) report_timeout(ctl);  // give up with what has been published
-        }
-        excl = op(excl, wave_allreduce(acc, op));
-        if (k0 < NW) break;
-        top -= first ? (int64_t)kLbPollWidth : (int64_t)NW * kWave;
-        first = false;
-    }
-    return excl;
-}
-
 // Plain scan tile: publish PARTIAL(agg), wait for the prefix, publish
 // INCLUSIVE(prefix op agg).  Returns the exclusive prefix (identity for
 // tile 0) in every lane.

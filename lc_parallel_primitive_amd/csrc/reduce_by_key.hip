@@ -22,10 +22,14 @@
 //      elements; entry 0 lacks the part of its run in earlier tiles) is
 //      gathered in LDS and stored contiguously into the tile's slot of a
 //      dense staging area.  Runs of mean 128 give 64 per tile.
-//    - A tile with more heads waits for the run count before it (walking
-//      back to the nearest tile that published an inclusive count) and the
-//      fold entering it (to the nearest tile with a head), publishes its
-//      inclusive count and writes its runs to the outputs directly.
+//    - A tile with more heads waits for the run count before it and the
+//      fold entering it (to the nearest tile with a head) and writes its runs
+//      to the outputs directly.  The run count is two-level: every tile adds
+//      its head count to its batch word (8 tiles) as it publishes, so a
+//      waiting tile sums its batch-mates' counts and walks the batch words
+//      back (whole batches add their totals) to batch 0 or to a batch whose
+//      last tile, having waited itself, published the inclusive count.  No
+//      tile waits for another tile's wait.
 //    The reference's single pass (reduce_by_key.h:90-258) waits on both
 //    look-backs in every tile.  On this part those waits cost ~130 of ~500
 //    us at 2^28 (int32 keys, f32 values, runs of mean 128): a tile here
@@ -53,11 +57,23 @@ constexpr uint32_t kRbkSlot = 128;  // runs a tile may stage (its dense slot)
 constexpr uint32_t kRbkHeadBit = 0x80000000u;   // summary count word: the tile has a head
 constexpr uint32_t kRbkDenseBit = 0x40000000u;  // summary count word: more than kRbkSlot heads
 constexpr uint32_t kRbkCountMask = 0x3FFFFFFFu;
+// Run-count batch words, 64-bit, one per kRbkBatch tiles: the low half is
+// (tiles arrived << 20) + their head counts (at most 8 x 8192 = 2^16), plus
+// kRbkGlobal once the batch's last tile has added the batch's inclusive run
+// count to the high half.
+constexpr uint32_t kRbkBatch = 8;
+constexpr uint64_t kRbkArrive = 1ull << 20;
+constexpr uint32_t kRbkGlobal = 0x80000000u;
+// Each batch word has a 128-byte line to itself (stride in words): with 8
+// words to a 64-byte line the atomic adds of 64 tiles queue on one line
+// (2^28 int32 keys, runs of mean 8: 937 us per call against 558 us padded;
+// runs of mean 128, where no tile waits: 367 against 353 us).
+constexpr uint32_t kRbkBwStride = 16;
 
 template <class K, class V>
 struct RbkLayout {
-    uint64_t tiles, groups, cwords_off, vwords_off, tcwords_off, tvwords_off, count_off, fold_off, pkeys_off,
-        pvals_off, total;
+    uint64_t tiles, groups, cwords_off, vwords_off, tcwords_off, tvwords_off, bwords_off, count_off, fold_off,
+        pkeys_off, pvals_off, total;
 };
 template <class K, class V>
 RbkLayout<K, V> rbk_layout(uint64_t n)
@@ -65,13 +81,15 @@ RbkLayout<K, V> rbk_layout(uint64_t n)
     RbkLayout<K, V> L{};
     L.tiles = bk_tiles<V>(n);
     L.groups = ceil_div(L.tiles, kRbkGroup);
-    // [status header | group look-back words | tile look-back words (all
-    //  zeroed by one fill) | tile summaries | dense slots]
+    // [status header | group look-back words | tile look-back words | batch
+    //  run-count words (all zeroed by one fill) | tile summaries | dense
+    //  slots]
     L.cwords_off = kStatusBytes;
     L.vwords_off = L.cwords_off + align_up(L.groups * 8, 256);
     L.tcwords_off = L.vwords_off + align_up(L.groups * 8 * lb_words<V>(), 256);
     L.tvwords_off = L.tcwords_off + align_up(L.tiles * 8, 256);
-    L.count_off = L.tvwords_off + align_up(L.tiles * 8 * lb_words<V>(), 256);
+    L.bwords_off = L.tvwords_off + align_up(L.tiles * 8 * lb_words<V>(), 256);
+    L.count_off = L.bwords_off + align_up(ceil_div(L.tiles, (uint64_t)kRbkBatch) * kRbkBwStride * 8, 256);
     L.fold_off = L.count_off + align_up(L.tiles * 4, 256);
     L.pkeys_off = L.fold_off + align_up(L.tiles * sizeof(V), 256);
     L.pvals_off = L.pkeys_off + align_up(L.tiles * kRbkSlot * sizeof(K), 256);
@@ -109,13 +127,93 @@ struct RbkSmem {
     uint32_t tc;
 };
 
+// Heads before `tile` (tile > 0, one wave): the counts of its batch-mates
+// before it (tile words, published before any wait) plus the batch words
+// before its batch, walked back in windows of 64 (the first round trip one
+// window, later ones kRbkWalkWindows) until batch 0 or a word carrying
+// kRbkGlobal (its inclusive count ends the walk); a batch word without it
+// must be complete (all kRbkBatch tiles arrived).  A late word is re-polled
+// (all late words of the round trip at once) up to the spin limit, then
+// counted as it is and reported.  Every lane returns the count.
+constexpr int kRbkWalkWindows = 8;
+__device__ uint32_t rbk_count_before(const uint64_t *tcwords, const uint64_t *bwords, uint32_t tile,
+                                     const WaitCtl &ctl)
+{
+    const uint32_t lane = lane_id();
+    const uint32_t b = tile / kRbkBatch, mates = tile % kRbkBatch;
+    const bool im = lane < mates;
+    uint64_t wm = im ? ld_relaxed(&tcwords[b * kRbkBatch + lane]) : 0ull;
+    uint32_t acc = 0;
+    int64_t top = (int64_t)b - 1;  // nearest batch not yet summed
+    uint32_t spins = 0;
+    for (bool first = true;; first = false) {
+        const int nw = first ? 1 : kRbkWalkWindows;
+        uint64_t w[kRbkWalkWindows];
+#pragma unroll
+        for (int k = 0; k < kRbkWalkWindows; ++k) {
+            const int64_t j = top - (int64_t)k * kWave - (int64_t)lane;
+            w[k] = k < nw && j >= 0 ? ld_relaxed(&bwords[j * kRbkBwStride]) : 0ull;
+        }
+        int k0 = kRbkWalkWindows;  // the nearest GLOBAL word (or batch 0's end): window k0, lane l0
+        uint32_t l0 = kWave;
+        bool late = false;
+        uint32_t v = 0;
+        for (;; ++spins) {
+            k0 = kRbkWalkWindows;
+            l0 = kWave;
+#pragma unroll
+            for (int k = kRbkWalkWindows - 1; k >= 0; --k) {
+                const int64_t j = top - (int64_t)k * kWave - (int64_t)lane;
+                const bool stop = k < nw && (j < 0 || ((uint32_t)w[k] & kRbkGlobal) != 0);
+                const uint64_t m = ballot(stop);
+                if (m) {
+                    k0 = k;
+                    l0 = (uint32_t)__builtin_ctzll(m);
+                }
+            }
+            late = first && im && (uint32_t)wm == kStInvalid;
+            v = 0;
+#pragma unroll
+            for (int k = 0; k < kRbkWalkWindows; ++k) {
+                const int64_t j = top - (int64_t)k * kWave - (int64_t)lane;
+                const bool in_range = k < nw && j >= 0 && (k < k0 || (k == k0 && lane <= l0));
+                if (!in_range) continue;
+                const uint32_t lo = (uint32_t)w[k];
+                if (lo & kRbkGlobal) v += (uint32_t)(w[k] >> 32);  // the stop word
+                else if ((lo >> 20) == kRbkBatch) v += lo & (uint32_t)(kRbkArrive - 1);
+                else late = true;
+            }
+            if (ballot(late) == 0) break;
+            if (spins + 1 >= ctl.spin_limit) {
+                if (lane == 0) report_timeout(ctl);  // count what has been published
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            if (first && im && (uint32_t)wm == kStInvalid) wm = ld_relaxed(&tcwords[b * kRbkBatch + lane]);
+#pragma unroll
+            for (int k = 0; k < kRbkWalkWindows; ++k) {
+                const int64_t j = top - (int64_t)k * kWave - (int64_t)lane;
+                if (k < nw && j >= 0 && ((uint32_t)w[k] & kRbkGlobal) == 0 &&
+                    ((uint32_t)w[k] >> 20) != kRbkBatch)
+                    w[k] = ld_relaxed(&bwords[j * kRbkBwStride]);
+            }
+        }
+        if (first) v += im ? (uint32_t)(wm >> 32) : 0u;
+        acc += wave_allreduce(v, SumOp());
+        if (k0 < kRbkWalkWindows || top - (int64_t)nw * kWave < 0) break;
+        top -= (int64_t)nw * kWave;
+    }
+    return acc;
+}
+
 template <class K, class V, class Op>
 __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict__ keys, const V *__restrict__ vin,
                                                             uint32_t n, uint32_t *__restrict__ tile_count,
                                                             V *__restrict__ tile_fold, K *__restrict__ pkeys,
                                                             V *__restrict__ pvals, K *__restrict__ unique_out,
                                                             V *__restrict__ agg_out, uint64_t *tcwords,
-                                                            uint64_t *tvwords, int vec_ok, WaitCtl ctl)
+                                                            uint64_t *tvwords, uint64_t *bwords, int vec_ok,
+                                                            WaitCtl ctl)
 {
     constexpr int VP = bk_vp<V>();
     constexpr uint32_t TILE = bk_tile<V>();
@@ -216,8 +314,11 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
             sm.tc = tc;
             tile_count[tile] = tc | (tf ? kRbkHeadBit : 0u) | (tc > kRbkSlot ? kRbkDenseBit : 0u);
             tile_fold[tile] = ts;
-            lb_publish(tcwords, tile, tc, tile == 0 ? kStInclusive : kStPartial, ctl);
+            lb_publish(tcwords, tile, tc, kStPartial, ctl);
             lb_publish(tvwords, tile, ts, tile == 0 || tf ? kStInclusive : kStPartial, ctl);
+            if (tile != ctl.withhold)  // a withheld tile publishes nothing (test hook)
+                __hip_atomic_fetch_add(&bwords[(tile / kRbkBatch) * kRbkBwStride], kRbkArrive + tc, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
@@ -227,13 +328,11 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
     const bool direct = sm.tc > kRbkSlot;
     if (direct) {
         if (wave == 0) {
-            uint32_t p = 0;
-            if (tile > 0) {
-                // staged tiles publish only PARTIAL counts: a tile after a
-                // long staged stretch walks it 512 words per round trip
-                p = lb_wait_prefix_wide<8>(tcwords, tile, SumOp(), 0u, ctl);
-                if (lane == 0) lb_publish(tcwords, tile, p + sm.tc, kStInclusive, ctl);
-            }
+            const uint32_t p = tile > 0 ? rbk_count_before(tcwords, bwords, tile, ctl) : 0u;
+            // the batch's last tile closes the batch's walk for later tiles
+            if (lane == 0 && tile % kRbkBatch == kRbkBatch - 1 && tile != ctl.withhold)
+                __hip_atomic_fetch_add(&bwords[(tile / kRbkBatch) * kRbkBwStride], ((uint64_t)(p + sm.tc) << 32) | kRbkGlobal,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (lane == 0) s_cpre = p;
         } else if (wave == 1) {
             const V p = tile > 0 ? lb_wait_prefix(tvwords, tile, op, ident, ctl) : ident;
@@ -555,6 +654,7 @@ int rbk_launch(void *temp, size_t tb, const void *keys_, const void *in_, void *
     uint64_t *vwords = reinterpret_cast<uint64_t *>(t + L.vwords_off);
     uint64_t *tcwords = reinterpret_cast<uint64_t *>(t + L.tcwords_off);
     uint64_t *tvwords = reinterpret_cast<uint64_t *>(t + L.tvwords_off);
+    uint64_t *bwords = reinterpret_cast<uint64_t *>(t + L.bwords_off);
     K *pkeys = reinterpret_cast<K *>(t + L.pkeys_off);
     V *pvals = reinterpret_cast<V *>(t + L.pvals_off);
     // the status header and both sets of look-back words are contiguous up
@@ -565,8 +665,8 @@ int rbk_launch(void *temp, size_t tb, const void *keys_, const void *in_, void *
     const int vec_ok = ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(in)) & 15) == 0;
     LCPP_LAUNCH("reduce_by_key_tile", s,
                 (rbk_tile_kernel<K, V, Op><<<(uint32_t)L.tiles, kBkBlock, 0, s>>>(
-                    keys, in, (uint32_t)n, tile_count, tile_fold, pkeys, pvals, uk, agg, tcwords, tvwords, vec_ok,
-                    ctl)));
+                    keys, in, (uint32_t)n, tile_count, tile_fold, pkeys, pvals, uk, agg, tcwords, tvwords, bwords,
+                    vec_ok, ctl)));
     LCPP_CHECK_LAUNCH();
     LCPP_LAUNCH("reduce_by_key_emit", s,
                 (rbk_emit_kernel<K, V, Op><<<(uint32_t)L.groups, kBkBlock, 0, s>>>(

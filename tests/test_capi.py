@@ -103,17 +103,18 @@ def test_temp_bytes_queries(L):
     assert rc == 0 and b == HDR + (1 << 15) * 8
     rc, b = _q(L.lcpp_scan_by_key_temp_bytes, 2, 5, 1 << 27)
     assert rc == 0 and b == HDR + (1 << 15) * 16
-    # reduce by key: head-count words + open-run words, each 256-byte aligned
     # reduce by key: look-back words per group of 64 tiles and per tile
-    # (count, fold), per-tile summaries (count word, fold), then the dense run
-    # slots (128 (key, value) entries per tile); each part 256-byte aligned
+    # (count, fold), run-count words per batch of 8 tiles (128 bytes each),
+    # per-tile summaries (count word, fold), then the dense run slots (128
+    # (key, value) entries per tile); each part 256-byte aligned
     def rbk(kb, vb, n, tile):
         tiles = -(-n // tile)
         groups = -(-tiles // 64)
+        batches = -(-tiles // 8)
         up = lambda x: -(-x // 256) * 256
         lbw = 1 if vb == 4 else 2
-        return (HDR + up(groups * 8) + up(groups * 8 * lbw) + up(tiles * 8) + up(tiles * 8 * lbw) + up(tiles * 4)
-                + up(tiles * vb) + up(tiles * 128 * kb) + up(tiles * 128 * vb))
+        return (HDR + up(groups * 8) + up(groups * 8 * lbw) + up(tiles * 8) + up(tiles * 8 * lbw) + up(batches * 128)
+                + up(tiles * 4) + up(tiles * vb) + up(tiles * 128 * kb) + up(tiles * 128 * vb))
     rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 0, 0, 1 << 28)
     assert rc == 0 and b == rbk(4, 4, 1 << 28, 8192)
     rc, b = _q(L.lcpp_reduce_by_key_temp_bytes, 5, 5, 100)

@@ -289,12 +289,14 @@ def test_reduce_by_key_direct_tile_densities(gpu, kdt, vdt, op):
         assert (uk[r:] == 0).all() and (ag[r:] == 0).all(), "write past the last run"
 
 
-@pytest.mark.parametrize("n_staged_tiles", [15, 16, 17, 600, 3000])
+@pytest.mark.parametrize("n_staged_tiles", [15, 16, 17, 600, 3000, 5000])
 def test_reduce_by_key_long_staged_prefix_then_dense(gpu, n_staged_tiles):
-    """A long stretch of tiles that stage their runs (they publish only
-    PARTIAL counts) followed by dense tiles, whose run-count look-back walks
-    the whole stretch: 15/16/17 tiles end the walk inside or just past its
-    first 16-word round trip; 600 and 3000 take several 512-word trips."""
+    """A long stretch of tiles that stage their runs (their batches of 8
+    tiles never get an inclusive run count) followed by dense tiles, whose
+    run-count walk adds up every batch of the stretch back to batch 0: the
+    dense part starts at the last, first and second tile of a batch
+    (15/16/17 tiles), and the walk takes one round trip of 64 batch words,
+    two (600, 3000 tiles: the second one of 512 words) or three (5000)."""
     tile = 8192
     n = (n_staged_tiles + 6) * tile + 333
     rng = np.random.default_rng(n_staged_tiles)
