@@ -344,14 +344,15 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
     const V vpre = direct ? s_vpre : ident;
 
     // pass 2: rescan from the slice prefixes; a head closes the run before it.
-    // STAGE (a direct tile with more runs than half its elements, keys in
-    // LDS, keys and values of one size): each (vector, wave) slice's runs go
-    // out through that slice's own part of sm.keys once its keys are read,
-    // so that consecutive lanes store consecutive runs.  A slice with at most
-    // half as many runs as elements puts keys and values there side by side
-    // and is stored after the last vector (one wait for all of them); a
-    // denser one goes out at once, keys then values.  Other direct tiles
-    // store each run where it closes.
+    // STAGE (a direct tile with more runs than a quarter of its elements,
+    // keys in LDS, keys and values of one size): each (vector, wave) slice's
+    // runs go out through that slice's own part of sm.keys once its keys are
+    // read, so that consecutive lanes store consecutive runs.  A slice with
+    // at most half as many runs as elements puts keys and values there side
+    // by side and is stored after the last vector (one wait for all of
+    // them); a denser one goes out at once, keys then values.  Other direct
+    // tiles store each run where it closes (staging from an eighth on cost
+    // 15 us at 2^28 with runs of mean 4).
     constexpr bool kStageDirect = kKeysInLds && sizeof(K) == sizeof(V);
     auto pass2 = [&](auto stage_tag) {
         constexpr bool STAGE = decltype(stage_tag)::value;
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
         }
     };
     if constexpr (kStageDirect) {
-        if (direct && sm.tc > TILE / 2) pass2(std::true_type{});
+        if (direct && sm.tc > TILE / 4) pass2(std::true_type{});
         else pass2(std::false_type{});
     } else {
         pass2(std::false_type{});

@@ -265,8 +265,8 @@ def test_reduce_by_key_dense_and_sparse_tiles_mixed(gpu, op):
 @pytest.mark.parametrize("op", ["sum", "min", "max"])
 def test_reduce_by_key_direct_tile_densities(gpu, kdt, vdt, op):
     """Tiles with more than 128 runs write them out themselves.  When more
-    than half of a tile's elements start a run (and keys and values have one
-    size) the runs go out through each wave slice's part of the tile's keys
+    than a quarter of a tile's elements start a run (and keys and values have
+    one size) the runs go out through each wave slice's part of the tile's keys
     in LDS: slices with at most half as many runs as elements together at the
     end of the tile, denser ones at once.  Densities on both sides of both
     boundaries, every key distinct, a ragged last tile, the first tile (whose
