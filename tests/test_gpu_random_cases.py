@@ -1,6 +1,7 @@
 """Seeded randomized parity cases for every primitive: random sizes (1 to
 2^20, log-uniform, plus 4 cases per group between 2^22 and 2^26), integer dtypes, value distributions (uniform, few
-distinct, AND-of-3, constant), sort directions, run lengths and segment
+distinct, AND-of-3, constant), sort directions, run lengths (one to three
+per input, for by-key) and segment
 layouts (tiling, random order, random windows with overlaps, gaps and
 inverted ranges).  Integer data, so every result is exact against the
 oracle.  A larger sweep of this kind (sizes to 2^25) found the gather load
@@ -114,21 +115,27 @@ def test_random_by_key(gpu, seed, lr):
     from lc_parallel_primitive_amd import DeviceReduce, DeviceScan
 
     rng, n, dt, kind = case_params(3000 + seed, lr)
-    run = int(rng.integers(1, 400))
-    keys = np.repeat(rng.integers(0, 4, size=n // run + 1), run)[:n].astype(dt)
-    vals = values(rng, np.int32, n, 1)
+    vdt = [np.int32, np.int64][int(rng.integers(0, 2))]
+    # run lengths: one per piece of the input, 1 to 3 pieces (so stretches of
+    # tiles that stage their runs meet stretches of tiles that write them)
+    pieces = int(rng.integers(1, 4))
+    bnd = np.concatenate([[0], np.sort(rng.integers(0, n + 1, size=pieces - 1)), [n]])
+    runs = [int(rng.integers(1, 8)) if rng.random() < 0.5 else int(rng.integers(1, 400)) for _ in range(pieces)]
+    keys = np.concatenate([np.repeat(rng.integers(0, 4, size=(b - a) // r + 1), r)[:b - a]
+                           for a, b, r in zip(bnd[:-1], bnd[1:], runs)]).astype(dt)
+    vals = values(rng, vdt, n, 1)
     op = ["sum", "min", "max"][rng.integers(0, 3)]
-    log(f"random by-key seed={seed} n={n} {np.dtype(dt).name} run={run} op={op}")
+    log(f"random by-key seed={seed} n={n} {np.dtype(dt).name}/{np.dtype(vdt).name} runs={runs} op={op}")
     dk, dv = g.to_dev(keys), g.to_dev(vals)
     s = DeviceScan()
-    so = g.empty(n, np.int32)
-    tmp = g.temp(DeviceScan.GetScanByKeyTempStorageBytes(np.dtype(dt).name, "int32", n))
+    so = g.empty(n, vdt)
+    tmp = g.temp(DeviceScan.GetScanByKeyTempStorageBytes(np.dtype(dt).name, np.dtype(vdt).name, n))
     for inclusive in (False, True):
         (s.InclusiveSumByKey if inclusive else s.ExclusiveSumByKey)(tmp, dk, dv, so, n)
         assert (g.to_host(so) == o.scan_by_key(keys, vals, inclusive)).all(), inclusive
-    uk, ag = g.empty(n, dt), g.empty(n, np.int32)
+    uk, ag = g.empty(n, dt), g.empty(n, vdt)
     nr = torch.zeros(1, dtype=torch.int32, device="cuda")
-    tmp = g.temp(DeviceReduce.GetReduceByKeyTempStorageBytes(np.dtype(dt).name, "int32", n))
+    tmp = g.temp(DeviceReduce.GetReduceByKeyTempStorageBytes(np.dtype(dt).name, np.dtype(vdt).name, n))
     DeviceReduce().ReduceByKey(tmp, dk, dv, uk, ag, nr, op, n)
     rk, rv = o.reduce_by_key(keys, vals, {"sum": o.OP_SUM, "min": o.OP_MIN, "max": o.OP_MAX}[op])
     m = int(nr.item())
