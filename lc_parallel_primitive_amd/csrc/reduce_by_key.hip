@@ -317,8 +317,8 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
             lb_publish(tcwords, tile, tc, kStPartial, ctl);
             lb_publish(tvwords, tile, ts, tile == 0 || tf ? kStInclusive : kStPartial, ctl);
             if (tile != ctl.withhold)  // a withheld tile publishes nothing (test hook)
-                __hip_atomic_fetch_add(&bwords[(tile / kRbkBatch) * kRbkBwStride], kRbkArrive + tc, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(&bwords[(tile / kRbkBatch) * kRbkBwStride], kRbkArrive + tc,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
@@ -331,8 +331,9 @@ __global__ __launch_bounds__(kBkBlock) void rbk_tile_kernel(const K *__restrict_
             const uint32_t p = tile > 0 ? rbk_count_before(tcwords, bwords, tile, ctl) : 0u;
             // the batch's last tile closes the batch's walk for later tiles
             if (lane == 0 && tile % kRbkBatch == kRbkBatch - 1 && tile != ctl.withhold)
-                __hip_atomic_fetch_add(&bwords[(tile / kRbkBatch) * kRbkBwStride], ((uint64_t)(p + sm.tc) << 32) | kRbkGlobal,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(&bwords[(tile / kRbkBatch) * kRbkBwStride],
+                                       ((uint64_t)(p + sm.tc) << 32) | kRbkGlobal, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
             if (lane == 0) s_cpre = p;
         } else if (wave == 1) {
             const V p = tile > 0 ? lb_wait_prefix(tvwords, tile, op, ident, ctl) : ident;
@@ -658,8 +659,8 @@ int rbk_launch(void *temp, size_t tb, const void *keys_, const void *in_, void *
     uint64_t *bwords = reinterpret_cast<uint64_t *>(t + L.bwords_off);
     K *pkeys = reinterpret_cast<K *>(t + L.pkeys_off);
     V *pvals = reinterpret_cast<V *>(t + L.pvals_off);
-    // the status header and both sets of look-back words are contiguous up
-    // to alignment padding: one fill
+    // the status header, both sets of look-back words and the batch
+    // run-count words are contiguous up to alignment padding: one fill
     if (lb_init(reinterpret_cast<uint64_t *>(t), L.count_off / 8, s, "reduce_by_key_init") != LCPP_OK)
         return LCPP_ERR_HIP;
     const WaitCtl ctl = wait_ctl(reinterpret_cast<uint32_t *>(t));
