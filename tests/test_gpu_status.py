@@ -178,23 +178,29 @@ def test_by_key_withheld_tile_reports_timeout(gpu):
     r = int(g.to_host(runs)[0])
     assert r == ek.size and (g.to_host(uk)[:r] == ek).all() and (g.to_host(agg)[:r] == ev).all()
 
-    # tiles with more than 128 runs wait in the tile launch itself: distinct
-    # keys, tile 4 withheld
-    n = 20 * 8192 + 3
+    # tiles with more than 128 runs wait in the tile launch itself for the
+    # counts of their batch-mates (batches of 8 tiles) and the words of the
+    # batches before them: distinct keys, and withheld tile 4 (a batch-mate of
+    # tiles 5-7) or tile 15 (batch 1's last tile: batch 1 never completes and
+    # never gets the inclusive count that tile would add, so every later
+    # tile's walk stalls on its word)
+    n = 40 * 8192 + 3
     keys = np.arange(n, dtype=np.int32)
     vals = g.random_array(np.int32, n, seed=6)
     dk, dv = g.to_dev(keys), g.to_dev(vals)
     uk, agg, runs = g.empty(n, np.int32), g.empty(n, np.int32), g.empty(1, np.uint32)
     t = _temp(L.lcpp_reduce_by_key_temp_bytes, 0, 0, n)
-    log("status: reduce by key, dense tiles, tile 4 withheld")
-    with withheld(4):
+    for tile in (4, 15):
+        log(f"status: reduce by key, dense tiles, tile {tile} withheld")
+        with withheld(tile):
+            assert L.lcpp_reduce_by_key(0, 0, 0, _p(t), t.numel(), _p(dk), _p(dv), _p(uk), _p(agg), _p(runs), n,
+                                        _sp()) == 0
+            assert status(t) == TIMEOUT
         assert L.lcpp_reduce_by_key(0, 0, 0, _p(t), t.numel(), _p(dk), _p(dv), _p(uk), _p(agg), _p(runs), n,
                                     _sp()) == 0
-        assert status(t) == TIMEOUT
-    assert L.lcpp_reduce_by_key(0, 0, 0, _p(t), t.numel(), _p(dk), _p(dv), _p(uk), _p(agg), _p(runs), n, _sp()) == 0
-    assert status(t) == OK
-    r = int(g.to_host(runs)[0])
-    assert r == n and (g.to_host(uk) == keys).all() and (g.to_host(agg) == vals).all()
+        assert status(t) == OK
+        r = int(g.to_host(runs)[0])
+        assert r == n and (g.to_host(uk) == keys).all() and (g.to_host(agg) == vals).all()
 
 
 def test_status_cleared_by_every_primitive(gpu):
