@@ -271,31 +271,33 @@ __device__ void rs_make_plan(const uint32_t *bins, uint32_t passes, uint64_t n, 
 }
 
 // ------------------------------------------------------------------ histogram
-// Counter layouts in LDS (128 KiB either way):
-//  * 4-byte keys, lane columns: lane l of every wave owns column l of a
-//    [P][128][64] table of 32-bit words, each holding the 16-bit counters of
-//    digits d and d + 128 (d < 128) of one pass.  A wave's counting atomic
-//    touches 64 distinct words in 64 distinct banks whatever the digits are
-//    (no bank conflicts, no same-address lanes).  A column counts at most 1/64
-//    of the keys a workgroup has seen since its last flush, so the table is
-//    flushed every kHistRoundSteps loop steps (4,177,920 keys < 64 x 65536).
-//  * 8-byte keys: [P][256][16], lane l counting into copy l % 16.
+// Counter layout in LDS, lane columns (128 KiB for either key size): a
+// [P][128][COLS] table of 32-bit words, each holding the 16-bit counters of
+// digits d and d + 128 (d < 128) of one pass; lane l of every wave counts in
+// column l % COLS.
+//  * 4-byte keys, COLS = 64: a wave's counting atomic touches 64 distinct
+//    words in 64 distinct banks whatever the digits are (no bank conflicts,
+//    no same-address lanes).
+//  * 8-byte keys (8 passes), COLS = 32: lanes l and l + 32 share a column,
+//    so at most two lanes of an atomic meet on one word.  Against 16 copies
+//    of a [P][256] table (lane l counting in copy l % 16; four lanes on one
+//    word whenever they share a digit, as every lane does on a constant key
+//    byte): SortPairs C4 (six constant key bytes) 1.694 -> 1.677 ms,
+//    full-range keys 5.816 -> 5.825 ms.
+// A column counts at most 1/COLS of the keys a workgroup has seen since its
+// last flush, so the table is flushed every kHistRoundSteps loop steps
+// (4-byte keys: 4,177,920 keys < 64 x 65536; 8-byte: 2,088,960 < 32 x 65536).
 template <class UK>
-constexpr bool hist_lane_columns()
+constexpr uint32_t hist_cols()
 {
-    return sizeof(UK) == 4;
-}
-template <class UK>
-constexpr int hist_copies()
-{
-    return 16;  // 8-byte keys
+    return sizeof(UK) == 4 ? 64u : 32u;
 }
 // Dynamic LDS: the counter table, then 17 words of planning state for the
 // last workgroup (the kernel has no static LDS).
 template <class UK>
 constexpr size_t hist_table_words()
 {
-    return hist_lane_columns<UK>() ? sizeof(UK) * (kRadix / 2) * kWave : sizeof(UK) * kRadix * hist_copies<UK>();
+    return sizeof(UK) * (kRadix / 2) * hist_cols<UK>();
 }
 template <class UK>
 constexpr size_t hist_lds_bytes()
@@ -310,8 +312,7 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     uint64_t clear_vecs, uint32_t *arrivals, uint32_t *__restrict__ hot, uint32_t *__restrict__ plan)
 {
     constexpr int P = sizeof(UK);
-    constexpr bool LC = hist_lane_columns<UK>();
-    constexpr int C = hist_copies<UK>();
+    constexpr uint32_t CO = hist_cols<UK>();
     constexpr uint32_t W = (uint32_t)hist_table_words<UK>();
     extern __shared__ uint32_t s_hist[];  // the counter table, then s_last, s_trivial[16]
     const uint32_t tid = threadIdx.x;
@@ -339,10 +340,7 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const uint32_t dg = digit_of<UK, KIND, DESC>(tk, p * kRadixBits);
-            if constexpr (LC)
-                atomicAdd(&s_hist[(((uint32_t)p * (kRadix / 2) + (dg & 127u)) << 6) + lane], dg & 128u ? 0x10000u : 1u);
-            else
-                atomicAdd(&s_hist[((uint32_t)p * kRadix + dg) * C + lane % C], 1u);
+            atomicAdd(&s_hist[((uint32_t)p * (kRadix / 2) + (dg & 127u)) * CO + lane % CO], dg & 128u ? 0x10000u : 1u);
         }
     };
     // one global add per non-zero bin (the sum of its counters); the table is
@@ -351,17 +349,12 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
         __syncthreads();
         for (uint32_t i = tid; i < (uint32_t)(P * kRadix); i += kHistBlock) {
             uint32_t c = 0;
-            if constexpr (LC) {
-                const uint32_t d = i % kRadix;
-                const uint32_t *col = s_hist + ((i / kRadix * (kRadix / 2) + (d & 127u)) << 6);
-                const uint32_t sh = (d >> 7) * 16u;
-                // threads of a wave start at different columns: no bank conflicts
+            const uint32_t d = i % kRadix;
+            const uint32_t *col = s_hist + (i / kRadix * (kRadix / 2) + (d & 127u)) * CO;
+            const uint32_t sh = (d >> 7) * 16u;
+            // threads of a wave start at different columns
 #pragma unroll 8
-                for (uint32_t k = 0; k < (uint32_t)kWave; ++k) c += (col[(k + d) & 63u] >> sh) & 0xFFFFu;
-            } else {
-#pragma unroll 8
-                for (int k = 0; k < C; ++k) c += s_hist[i * C + k];
-            }
+            for (uint32_t k = 0; k < CO; ++k) c += (col[(k + d) % CO] >> sh) & 0xFFFFu;
             if (c) __hip_atomic_fetch_add(&bins[i], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         if (more) {
@@ -374,7 +367,7 @@ __global__ __launch_bounds__(kHistBlock) void rs_histogram_kernel(
     constexpr uint64_t step = (uint64_t)kHistBlock * V * kVecs;
     const bool vec = (reinterpret_cast<uintptr_t>(keys) & 15) == 0;
     // rounds of whole steps (every round but the last is a multiple of the step)
-    const uint64_t round_len = LC ? kHistRoundSteps * step : ~0ull;
+    const uint64_t round_len = kHistRoundSteps * step;
     for (uint64_t r0 = b0; r0 < b1;) {
         const uint64_t r1 = b1 - r0 > round_len ? r0 + round_len : b1;
         uint64_t tail = r0;
