@@ -146,7 +146,12 @@ def test_graph_by_key_and_segments(gpu):
 
     def set_input(r):
         rng = np.random.default_rng(4000 + r)
-        keys = np.cumsum(rng.random(n) < 1 / (5 + 40 * (r + 1))).astype(np.int32)  # runs, their length varies per replay
+        # runs whose mean length varies per replay: ReduceByKey tiles with a
+        # few runs (staged), with more than 128 (they take their run count from
+        # the batch words), and with more than a quarter of their elements
+        # starting runs (stored through LDS)
+        mean = {-1: 45.0, 0: 1.5, 1: 85.0, 2: 3.0}[r]
+        keys = np.cumsum(rng.random(n) < 1 / mean).astype(np.int32)
         vals = rng.integers(-1000, 1000, n).astype(np.int32)
         bb = np.sort(rng.integers(0, n, S)).astype(np.uint32)
         ee = np.minimum(bb.astype(np.int64) + rng.integers(0, 400, S), n).astype(np.uint32)
