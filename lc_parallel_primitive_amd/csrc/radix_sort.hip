@@ -494,8 +494,12 @@ void rs_onesweep_kernel(RsBuffers<UK, UV> buf, uint32_t n, uint32_t shift, const
     constexpr int WAVE_ITEMS = kWave * IPT;
     constexpr int kSleep = PAIRS ? 4 : 16;
     // batch words per look-back poll: 2 keeps the 16384-key kernel within
-    // 80 VGPRs (a window of 4 spills 20 VGPRs: 2.59 ms per sort; 3: same as 2)
-    constexpr int kWindow = 2;
+    // 80 VGPRs (a window of 4 spills 20 VGPRs: 2.59 ms per sort; 3: same as 2).
+    // Pairs kernels at four waves per SIMD have registers to spare and read
+    // 8: their walk spans ~8 batch words, and a wave walks until its slowest
+    // digit ends (SortPairs u64 -> u32 at 2^27, all 8 passes: 5851 -> 5805
+    // us; 6 of 8 passes skipped: 1686 -> 1676 us; a window of 4 gains half).
+    constexpr int kWindow = PAIRS && os_waves_per_eu<UK, UV, PAIRS, MATCH>() == 4 ? 8 : 2;
     static_assert(TILE <= 65536, "tile ranks are packed in 16 bits");
     __shared__ OnesweepSmem<IPT, UK, UV> sm;
 
