@@ -118,11 +118,14 @@ def test_pairs_stable_vs_oracle(gpu, kdt, vdt, n):
 
 
 # Tiles hold 16384 keys (8192 when keys or values are 8 bytes) and the look-back
-# groups them in batches of 8: sizes around 1, 2, 3 and 5 batches, ragged and exact.
+# groups them in batches of 8: sizes around 1, 2, 3, 5, 8, 9 and 25 batches,
+# ragged and exact (a walk reads up to 8 batch words per poll in the kernels
+# at four waves per SIMD, so the walks from batch 8 on take the unguarded
+# window).
 @pytest.mark.parametrize("kdt,vdt", [(np.uint32, None), (np.uint64, None), (np.uint32, np.uint32),
                                      (np.uint64, np.uint32)])
 @pytest.mark.parametrize("tiles,delta", [(7, 0), (8, -1), (8, 0), (8, 1), (9, 0), (16, 0), (17, 5),
-                                         (24, -3), (40, 7)])
+                                         (24, -3), (40, 7), (64, 0), (65, -1), (72, 3), (200, 11)])
 def test_lookback_batch_boundaries(gpu, kdt, vdt, tiles, delta):
     import gpu_util as g
 
